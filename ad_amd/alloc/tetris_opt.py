@@ -110,9 +110,11 @@ def tetris_opt(proc):
             return node
         for idx in range(len(node.kargs)):
             for entry in entries:
+                _tag(node.kargs[idx], entry)
                 node.kargs[idx].rename(entry.var_id, temp_id, _add_offset(entry.offset))
         for entry in entries:
             if not node.kres.is_none():
+                _tag(node.kres, entry)
                 node.kres.rename(entry.var_id, temp_id, _add_offset(entry.offset))
         return node
     proc.walk(replace_to_temp)
@@ -120,6 +122,18 @@ def tetris_opt(proc):
     if max_temp_size > 0:
         proc.insert(0, AllocEntry(temp_id, max_temp_size, content=None))
         proc.append(DeallocEntry(temp_id, max_temp_size))
+
+
+def _tag(karg, entry):
+    """Remember which packed variable (id, offset, size) an operand addresses,
+    for the backend's aliasing checks.  Does not change the IR."""
+    from ..kernalize import KConcat, KMatrix
+    if isinstance(karg, KMatrix):
+        if karg.id == entry.var_id:
+            karg.tetris_var = (entry.var_id, entry.offset, entry.size)
+    elif isinstance(karg, KConcat):
+        _tag(karg.karg_one, entry)
+        _tag(karg.karg_two, entry)
 
 
 def _add_offset(offset):

@@ -1,0 +1,715 @@
+"""Lowering of procedural-IR commands to specialised HIP kernels.
+
+For every command this module produces one or more ``KernelPlan``s: a
+canonical HIP source (compiled through hipRTC, deduplicated by text), a
+launch geometry and an argument list of arena byte offsets and integers.
+
+Statement semantics follow the reference kernel templates
+(autodiff/device/opencl/kernels/*.py): a fused command is an ordered list of
+statements ``kres = f(kargs)`` evaluated per element; temps are registers;
+constants are double literals (``str(float)``), so ``x * c`` is computed in
+double and rounded to float, exactly as the OpenCL source does.
+
+Where the reference relies on all work-items of a work-group running in
+lockstep -- a statement writing a region that another element of the same
+kernel still reads, which the tetris allocator produces when a value dies
+inside a fused group -- the command is emitted as a sequence of kernels,
+one per statement, each staging its result before storing it
+(``lockstep`` plans).  ``hazards`` decides which commands need that.
+"""
+import hashlib
+import math
+from dataclasses import dataclass, field
+from math import ceil, prod
+from typing import Dict, List, Optional, Tuple
+
+from ...alloc import AllocEntry
+from ...expr import (Add, BitwiseAnd, Constant, Div, Global, LessThan, Minus, MoreThan, Mult,
+                     Remainder, ShiftLeft, ShiftRight, Val, X, Y)
+from ...fusion import DPElwFuse, ElwFuse, ReduceElwFuse
+from ...graph import (BinaryNode, BinaryOp, ContigiousNode, DotProdNode, ReduceNode, ReduceOp,
+                      UnaryNode, UnaryOp)
+from ...kernalize import KConcat, KConstant, KMatrix
+from .analysis import AFF, INV, const_of, split_const, upper_bound, vec_class
+
+BLOCK = 256
+
+_OPS = {Add: "+", Minus: "-", Mult: "*", Div: "/", Remainder: "%", ShiftRight: ">>",
+        ShiftLeft: "<<", BitwiseAnd: "&", MoreThan: ">", LessThan: "<"}
+
+
+# ------------------------------------------------------------------ plans
+@dataclass
+class KernelPlan:
+    source: str                   # full source; kernel is named KNAME
+    grid: Tuple[int, int, int]
+    block: Tuple[int, int, int]
+    args: List[tuple]             # ("buf", buffer_id, float_offset) | ("scratch", float_offset) | ("int", v)
+    shared: int = 0
+    family: str = ""              # "elw" | "reduce" | "dotprod" | "copy"
+    flops: int = 0                # algorithmic flops (dotprod) for reporting
+    bytes: int = 0                # algorithmic bytes for reporting
+
+    @property
+    def key(self):
+        return hashlib.sha1(self.source.encode()).hexdigest()[:20]
+
+
+# ------------------------------------------------------------------ statements
+def statements(nodes):
+    """``[(kind, node)]`` with kind ``bin``/``un``/``copy``/``tmp``/``init``."""
+    out = []
+    for n in nodes:
+        if isinstance(n, BinaryNode):
+            out.append(("bin", n))
+        elif isinstance(n, UnaryNode):
+            out.append(("un", n))
+        elif isinstance(n, ContigiousNode):
+            out.append(("copy", n))
+        elif isinstance(n, AllocEntry):
+            assert n.is_temp, "non-temp alloc entry inside a fused command"
+            out.append(("tmp", n))
+        elif isinstance(n, (DotProdNode, ReduceNode)):
+            out.append(("init", n))
+    return out
+
+
+def _iter_kmatrix(karg):
+    if isinstance(karg, KMatrix):
+        yield karg
+    elif isinstance(karg, KConcat):
+        yield from _iter_kmatrix(karg.karg_one)
+        yield from _iter_kmatrix(karg.karg_two)
+
+
+# ------------------------------------------------------------------ hazards
+class BufferInfo:
+    """Per buffer id: total floats, and per tetris variable region."""
+
+    def __init__(self):
+        self.size: Dict[int, int] = {}
+
+
+def _region(km: KMatrix, buffers: BufferInfo):
+    var = getattr(km, "tetris_var", None)
+    if var is not None:
+        _, off, size = var
+        return (km.id, off, off + size), var[0]
+    return (km.id, 0, buffers.size.get(km.id, 1 << 62)), ("buf", km.id)
+
+
+def _same_map(a: KMatrix, b: KMatrix) -> bool:
+    return a.id == b.id and repr(a.access) == repr(b.access)
+
+
+def hazards(stmts, buffers: BufferInfo, index_kind: str) -> bool:
+    """True when some element of the command may read or write a location
+    that another element writes (cross-element dependence through memory).
+
+    Two accesses on disjoint regions never conflict; two accesses to the same
+    location expression of the same variable touch the same element.  A
+    DotProd/Reduce operand is read for whole rows/columns, so any write
+    overlapping it is a conflict."""
+    reads, writes = [], []
+    for kind, n in stmts:
+        if kind == "tmp":
+            continue
+        whole = kind == "init"
+        for k in n.kargs:
+            for km in _iter_kmatrix(k):
+                if not km.is_temp:
+                    reads.append((km, whole))
+        if not n.kres.is_none() and not n.kres.is_temp:
+            writes.append((n.kres, kind == "init" and index_kind == "xy"))
+    for w, _ in writes:
+        wr, wv = _region(w, buffers)
+        for r, whole in reads + [(x, False) for x, _ in writes if x is not w]:
+            rr, rv = _region(r, buffers)
+            if rr[0] != wr[0] or rr[2] <= wr[1] or wr[2] <= rr[1]:
+                continue
+            if not whole and wv == rv and _same_map(w, r):
+                continue
+            return True
+    return False
+
+
+# ------------------------------------------------------------------ lowering helpers
+class Params:
+    """Kernel pointer parameters keyed by (buffer id, folded offset)."""
+
+    def __init__(self):
+        self.slots: List[tuple] = []
+        self.index: Dict[tuple, int] = {}
+
+    def ptr(self, kind, ident, offset) -> str:
+        key = (kind, ident, offset)
+        if key not in self.index:
+            self.index[key] = len(self.slots)
+            self.slots.append(key)
+        return f"p{self.index[key]}"
+
+
+def lower_index(e, ity) -> str:
+    c = const_of(e)
+    if c is not None:
+        return f"(({ity}){int(c)})"
+    if isinstance(e, Global):
+        return "_global_id"
+    if isinstance(e, X):
+        return "_x"
+    if isinstance(e, Y):
+        return "_y"
+    if type(e) is Val:
+        return lower_index(e.v, ity)
+    op = _OPS[type(e)]
+    return f"({lower_index(e.a, ity)} {op} {lower_index(e.b, ity)})"
+
+
+def const_literal(c) -> str:
+    """The reference emits ``str(constant)``: a double literal for floats."""
+    if isinstance(c, float):
+        if math.isinf(c) or math.isnan(c):
+            return "(__builtin_huge_val())" if c > 0 else ("(-__builtin_huge_val())" if c < 0 else "(__builtin_nan(\"\"))")
+        return repr(c)
+    return str(c)
+
+
+def _scratch_km(off, access=None):
+    km = KMatrix(-1, access if access is not None else Global(), [1])
+    km.scratch_offset = off
+    return km
+
+
+class Lowerer:
+    """Emits scalar C++ for operands and statements of one kernel."""
+
+    def __init__(self, ity, params: Params):
+        self.ity = ity
+        self.params = params
+        self.forward: Dict[tuple, str] = {}   # location key -> register holding its value
+        self.nreg = 0
+
+    def _loc(self, km: KMatrix):
+        core, c = split_const(km.access)
+        if getattr(km, "scratch_offset", None) is not None:
+            p = self.params.ptr("scratch", 0, km.scratch_offset + c)
+        else:
+            p = self.params.ptr("buf", km.id, c)
+        idx = lower_index(core, self.ity)
+        return p, idx, (p, repr(core))
+
+    def operand(self, karg) -> str:
+        if isinstance(karg, KConstant):
+            return const_literal(karg.constant)
+        if isinstance(karg, KConcat):
+            cond = lower_index(karg.condition, self.ity)
+            return f"({cond} ? ({self.operand(karg.karg_two)}) : ({self.operand(karg.karg_one)}))"
+        if karg.is_temp:
+            return f"temp_{karg.id}"
+        p, idx, key = self._loc(karg)
+        if key in self.forward:
+            return self.forward[key]
+        return f"{p}[{idx}]"
+
+    def rhs(self, kind, n, init_value) -> str:
+        if kind == "bin":
+            op = "+" if n.op == BinaryOp.ADD else "*"
+            return f"{self.operand(n.kargs[0])} {op} {self.operand(n.kargs[1])}"
+        if kind == "copy":
+            return self.operand(n.kargs[0])
+        if kind == "init":
+            return init_value
+        a = self.operand(n.kargs[0])
+        op = n.op
+        if op == UnaryOp.EXP2:
+            return f"exp2({a})"
+        if op == UnaryOp.LOG2:
+            return f"log2({a})"
+        if op == UnaryOp.SIN:
+            return f"sin({a})"
+        if op == UnaryOp.RECIP:
+            return f"1.0/{a}"
+        if op == UnaryOp.SQRT:
+            return f"sqrt(fabs({a}))"
+        cmp = {UnaryOp.EQUAL: "==", UnaryOp.MORE_ZERO: ">", UnaryOp.LESS_ZERO: "<",
+               UnaryOp.MORE_OR_EQ_ZERO: ">=", UnaryOp.LESS_OR_EQ_ZERO: "<="}[op]
+        return f"({a} {cmp} 0.0f) ? 1.0 : 0.0"
+
+    def statements(self, stmts, init_value) -> List[str]:
+        """Per-element statement list with store-to-load forwarding; stores of
+        non-temp results are emitted in program order (a later store to the
+        same location wins)."""
+        lines = []
+        for kind, n in stmts:
+            if kind == "tmp":
+                lines.append(f"float temp_{n.id} = 0.0f;")
+                continue
+            value = self.rhs(kind, n, init_value)
+            if n.kres.is_temp:
+                lines.append(f"temp_{n.kres.id} = {value};")
+                continue
+            r = f"r{self.nreg}"
+            self.nreg += 1
+            lines.append(f"const float {r} = {value};")
+            p, idx, key = self._loc(n.kres)
+            lines.append(f"{p}[{idx}] = {r};")
+            self.forward[key] = r
+        return lines
+
+
+def _ity(bound) -> str:
+    return "unsigned" if bound < (1 << 31) else "unsigned long long"
+
+
+def _expr_bound(stmts, gmax, xmax, ymax):
+    b = max(gmax, xmax, ymax, 1)
+    for kind, n in stmts:
+        if kind == "tmp":
+            continue
+        ks = list(n.kargs) + ([n.kres] if not n.kres.is_none() else [])
+        for k in ks:
+            for km in _iter_kmatrix(k):
+                b = max(b, upper_bound(km.access, gmax, xmax, ymax))
+            if isinstance(k, KConcat):
+                b = max(b, upper_bound(k.condition, gmax, xmax, ymax))
+    return b
+
+
+def _params_decl(params: Params) -> str:
+    return ", ".join(f"float* p{i}" for i in range(len(params.slots)))
+
+
+def _plan_args(params: Params, extra_ints=()) -> List[tuple]:
+    out = []
+    for kind, ident, off in params.slots:
+        out.append(("scratch", off) if kind == "scratch" else ("buf", ident, off))
+    out.extend(("int", v) for v in extra_ints)
+    return out
+
+
+KNAME = "adhip_kernel"
+
+
+# ------------------------------------------------------------------ ElwFuse family
+def _vector_plan(stmts, n):
+    """Lane layout for 4 elements per thread: every non-temp access must be
+    contiguous-aligned or constant over aligned groups of 4, with its folded
+    offset a multiple of 4 floats."""
+    if n % 4 != 0:
+        return False
+    for kind, node in stmts:
+        if kind == "tmp":
+            continue
+        ks = list(node.kargs) + [node.kres]
+        for k in ks:
+            if isinstance(k, KConcat):
+                return False
+            if isinstance(k, KMatrix) and not k.is_temp:
+                core, c = split_const(k.access)
+                vc = vec_class(core, Global)
+                if vc.kind == AFF and vc.al and c % 4 == 0:
+                    continue
+                if vc.kind == INV and k is not node.kres:
+                    continue
+                return False
+    return True
+
+
+def elementwise_plan(stmts, n, index_kind="global", n_cols=1, flops=0) -> KernelPlan:
+    """One thread per element (or per 4 elements when every access allows a
+    float4), statements in order.  ``index_kind`` defines ``_x``/``_y`` for
+    statements lifted out of a DotProd (``dp``: row = g / n_cols) or Reduce
+    (``red``: row = g) command."""
+    params = Params()
+    bound = _expr_bound(stmts, max(n - 1, 0), max(n - 1, 0), max(n_cols - 1, 0))
+    ity = _ity(bound)
+    setup = ""
+    if index_kind == "dp":
+        setup = (f"const {ity} _x = _global_id / ({ity}){n_cols}; "
+                 f"const {ity} _y = _global_id % ({ity}){n_cols}; (void)_x; (void)_y;")
+    elif index_kind == "red":
+        setup = f"const {ity} _x = _global_id; const {ity} _y = 0; (void)_x; (void)_y;"
+    vec = index_kind == "global" and _vector_plan(stmts, n)
+    if not vec:
+        low = Lowerer(ity, params)
+        body = "\n    ".join(low.statements(stmts, None))
+        src = f"""extern "C" __global__ void __launch_bounds__({BLOCK}) {KNAME}({_params_decl(params)}{', ' if params.slots else ''}unsigned long long n_) {{
+  const {ity} _global_id = ({ity})blockIdx.x * {BLOCK}u + threadIdx.x;
+  if (_global_id >= ({ity})n_) return;
+  {setup}
+  {body}
+}}
+"""
+        grid = (max(1, ceil(n / BLOCK)), 1, 1)
+    else:
+        src = _vector_source(stmts, ity, params)
+        grid = (max(1, ceil(n / (4 * BLOCK))), 1, 1)
+    return KernelPlan(src, grid, (BLOCK, 1, 1), _plan_args(params, (n,)), family="elw", flops=flops)
+
+
+def _vector_source(stmts, ity, params: Params) -> str:
+    """Four consecutive elements per thread: float4 loads/stores for aligned
+    contiguous accesses, one scalar load for group-constant accesses."""
+    lines = []
+    loaded: Dict[tuple, str] = {}
+    written: Dict[tuple, str] = {}
+    temps = []
+    cnt = [0]
+
+    def fresh(prefix):
+        cnt[0] += 1
+        return f"{prefix}{cnt[0]}"
+
+    def loc(km):
+        core, c = split_const(km.access)
+        p = params.ptr("buf", km.id, c)
+        return p, core, (p, repr(core))
+
+    def operand(k):
+        if isinstance(k, KConstant):
+            lit = const_literal(k.constant)
+            return [lit] * 4
+        if k.is_temp:
+            return [f"temp_{k.id}[{i}]" for i in range(4)]
+        p, core, key = loc(k)
+        if key in written:
+            return [f"{written[key]}.{c}" for c in "xyzw"]
+        if key in loaded:
+            return loaded[key]
+        vc = vec_class(core, Global)
+        idx = lower_index(core, ity)
+        if vc.kind == AFF:
+            v = fresh("v")
+            lines.append(f"const float4 {v} = *reinterpret_cast<const float4*>({p} + {idx});")
+            vals = [f"{v}.{c}" for c in "xyzw"]
+        else:
+            v = fresh("s")
+            lines.append(f"const float {v} = {p}[{idx}];")
+            vals = [v] * 4
+        loaded[key] = vals
+        return vals
+
+    def rhs(kind, n, lane):
+        def op(k):
+            return operand(k)[lane]
+        if kind == "bin":
+            o = "+" if n.op == BinaryOp.ADD else "*"
+            return f"{op(n.kargs[0])} {o} {op(n.kargs[1])}"
+        if kind == "copy":
+            return op(n.kargs[0])
+        a = op(n.kargs[0])
+        u = n.op
+        if u == UnaryOp.EXP2:
+            return f"exp2({a})"
+        if u == UnaryOp.LOG2:
+            return f"log2({a})"
+        if u == UnaryOp.SIN:
+            return f"sin({a})"
+        if u == UnaryOp.RECIP:
+            return f"1.0/{a}"
+        if u == UnaryOp.SQRT:
+            return f"sqrt(fabs({a}))"
+        cmp = {UnaryOp.EQUAL: "==", UnaryOp.MORE_ZERO: ">", UnaryOp.LESS_ZERO: "<",
+               UnaryOp.MORE_OR_EQ_ZERO: ">=", UnaryOp.LESS_OR_EQ_ZERO: "<="}[u]
+        return f"({a} {cmp} 0.0f) ? 1.0 : 0.0"
+
+    for kind, n in stmts:
+        if kind == "tmp":
+            temps.append(n.id)
+            lines.append(f"float temp_{n.id}[4] = {{0.0f, 0.0f, 0.0f, 0.0f}};")
+            continue
+        # operands are loaded before the statement computes (program order)
+        for k in n.kargs:
+            operand(k)
+        vals = [rhs(kind, n, i) for i in range(4)]
+        if n.kres.is_temp:
+            for i in range(4):
+                lines.append(f"temp_{n.kres.id}[{i}] = {vals[i]};")
+            continue
+        p, core, key = loc(n.kres)
+        r = fresh("w")
+        lines.append(f"float4 {r}; {r}.x = {vals[0]}; {r}.y = {vals[1]}; {r}.z = {vals[2]}; {r}.w = {vals[3]};")
+        lines.append(f"*reinterpret_cast<float4*>({p} + {lower_index(core, ity)}) = {r};")
+        written[key] = r
+        loaded.pop(key, None)
+    body = "\n  ".join(lines)
+    return f"""extern "C" __global__ void __launch_bounds__({BLOCK}) {KNAME}({_params_decl(params)}{', ' if params.slots else ''}unsigned long long n_) {{
+  const {ity} _global_id = (({ity})blockIdx.x * {BLOCK}u + threadIdx.x) * 4u;
+  if (_global_id >= ({ity})n_) return;
+  {body}
+}}
+"""
+
+
+# ------------------------------------------------------------------ DotProd+Elw family
+def _loader_struct(name, karg, role, params: Params, ity, dims) -> Tuple[str, bool]:
+    """Functor ``name`` with ``at(_x, _y)`` for a DotProd operand.  ``role``
+    'A': (_x, _y) = (m, k); 'B': (_x, _y) = (k, n).  Returns (source, vec)."""
+    M_or_K, second = dims
+    if isinstance(karg, KConstant):
+        return (f"struct {name} {{ static constexpr int kMode = 0; static constexpr bool kVec = false; @FIELDS@\n"
+                f"  __device__ float at({ity} _x, {ity} _y) const {{ (void)_x; (void)_y; return (float)({const_literal(karg.constant)}); }}\n"
+                f"  __device__ float4 at4({ity}, {ity}) const {{ return make_float4(0.f, 0.f, 0.f, 0.f); }} }};\n"), False
+    low = Lowerer(ity, params)
+    if isinstance(karg, KConcat):
+        expr = low.operand(karg)
+        return (f"struct {name} {{ static constexpr int kMode = 0; static constexpr bool kVec = false; @FIELDS@\n"
+                f"  __device__ float at({ity} _x, {ity} _y) const {{ (void)_x; (void)_y; return (float)({expr}); }}\n"
+                f"  __device__ float4 at4({ity}, {ity}) const {{ return make_float4(0.f, 0.f, 0.f, 0.f); }} }};\n"), False
+    assert isinstance(karg, KMatrix) and not karg.is_temp, "DotProd operand must be a buffer or constant"
+    core, c = split_const(karg.access)
+    p = params.ptr("buf", karg.id, c)
+    idx = lower_index(core, ity)
+    # A: mode 0 contiguous along k (= _y); B: mode 0 contiguous along n (= _y)
+    vy = vec_class(core, Y)
+    vx = vec_class(core, X)
+    if vy.kind == AFF:
+        mode = 0
+        vec = vy.al and c % 4 == 0 and second % 4 == 0
+    elif vx.kind == AFF:
+        mode = 1
+        vec = vx.al and c % 4 == 0 and M_or_K % 4 == 0
+    else:
+        mode, vec = 0, False
+    if role == "B":
+        mode = 0 if mode == 0 else 1
+    src = (f"struct {name} {{ static constexpr int kMode = {mode}; static constexpr bool kVec = {'true' if vec else 'false'}; @FIELDS@\n"
+           f"  __device__ float at({ity} _x, {ity} _y) const {{ return {p}[{idx}]; }}\n"
+           f"  __device__ float4 at4({ity} _x, {ity} _y) const {{ return *reinterpret_cast<const float4*>({p} + {idx}); }} }};\n")
+    return src, vec
+
+
+def _fields(params: Params) -> str:
+    return " ".join(f"float* p{i};" for i in range(len(params.slots)))
+
+
+def _init_list(params: Params) -> str:
+    return ", ".join(f"p{i}" for i in range(len(params.slots)))
+
+
+def dotprod_plan(stmts, dp, flops_only=False) -> KernelPlan:
+    """DotProd (+ elementwise epilogue) on fp32 MFMA tiles
+    (kernels/dotprod.py:7-43, dp_elw_fuse.py:26-65 semantics)."""
+    M, N = dp.shape
+    K = dp.children_shapes[0][1]
+    bound = _expr_bound(stmts, M * N, max(M, K), max(N, K))
+    ity = _ity(bound)
+    params = Params()
+    la, _ = _loader_struct("LA", dp.kargs[0], "A", params, ity, (M, K))
+    lb, _ = _loader_struct("LB", dp.kargs[1], "B", params, ity, (K, N))
+    low = Lowerer(ity, params)
+    body = "\n    ".join(low.statements(stmts, "_value"))
+    epi = (f"struct EPI {{ @FIELDS@\n"
+           f"  __device__ void operator()(float _value, {ity} _x, {ity} _y) const {{\n"
+           f"    const {ity} _global_id = _x * ({ity}){N} + _y; (void)_global_id;\n    {body}\n  }} }};\n")
+    init = _init_list(params)
+    src = ((la + lb + epi).replace("@FIELDS@", _fields(params)) +
+           f"extern \"C\" __global__ void __launch_bounds__(256) {KNAME}({_params_decl(params)}) {{\n"
+           f"  adhip::dp_mfma(LA{{{init}}}, LB{{{init}}}, EPI{{{init}}}, {M}, {N}, {K});\n}}\n")
+    grid = (ceil(N / 128), ceil(M / 128), 1)
+    return KernelPlan(src, grid, (256, 1, 1), _plan_args(params), family="dotprod",
+                      flops=2 * M * N * K)
+
+
+# ------------------------------------------------------------------ Reduce+Elw family
+def tree_inclusion(R):
+    """Elements of a row that reach slot 0 of the reference's work-group tree
+    (reduce.py:33-43 with L = ceil(R/2)*2), as a sorted list of indices in
+    [0, L); indices >= R are zero padding."""
+    L = ceil(R / 2) * 2
+    if L & (L - 1) == 0:
+        return list(range(L))
+    sets = [{y} for y in range(L)]
+    off = L // 2
+    while off > 0:
+        for y in range(off):
+            sets[y] |= sets[y + off]
+        off >>= 1
+    return sorted(sets[0])
+
+
+def reduce_plan(stmts, red) -> KernelPlan:
+    """Row reduction (+ epilogue on the reduced value)
+    (kernels/reduce.py:8-66, reduce_elw_fuse.py:12-80 semantics)."""
+    V, R = red.children_shapes[0]
+    inc = tree_inclusion(R)
+    dropped = [y for y in range(R) if y not in set(inc)] if len(inc) < R else []
+    pad_zero = any(y >= R for y in inc)
+    bound = _expr_bound(stmts, V, V, R)
+    ity = _ity(bound)
+    params = Params()
+    karg = red.kargs[0]
+    mode = "rows"
+    vec = False
+    if isinstance(karg, KConstant):
+        at = f"return (float)({const_literal(karg.constant)});"
+        at4 = "return make_float4(0.f, 0.f, 0.f, 0.f);"
+    else:
+        low0 = Lowerer(ity, params)
+        if isinstance(karg, KConcat):
+            at = f"return (float)({low0.operand(karg)});"
+            at4 = "return make_float4(0.f, 0.f, 0.f, 0.f);"
+        else:
+            core, c = split_const(karg.access)
+            p = params.ptr("buf", karg.id, c)
+            idx = lower_index(core, ity)
+            at = f"return {p}[{idx}];"
+            at4 = f"return *reinterpret_cast<const float4*>({p} + {idx});"
+            vy = vec_class(core, Y)
+            vx = vec_class(core, X)
+            if vy.kind == AFF:
+                vec = vy.al and c % 4 == 0 and R % 4 == 0 and not dropped
+            elif vx.kind == AFF:
+                mode = "cols"
+    if dropped:
+        words = [0] * ((R + 31) // 32)
+        for y in inc:
+            if y < R:
+                words[y >> 5] |= 1 << (y & 31)
+        table = ", ".join(f"{w}u" for w in words)
+        inc_fn = (f"  __device__ bool inc({ity} y) const {{ constexpr unsigned t[] = {{{table}}}; "
+                  f"return (t[y >> 5] >> (y & 31)) & 1u; }}\n")
+    else:
+        inc_fn = f"  __device__ bool inc({ity}) const {{ return true; }}\n"
+    ld = (f"struct LD {{ static constexpr bool kVec = {'true' if vec else 'false'}; @FIELDS@\n"
+          f"  __device__ float at({ity} _x, {ity} _y) const {{ (void)_x; (void)_y; {at} }}\n"
+          f"  __device__ float4 at4({ity} _x, {ity} _y) const {{ (void)_x; (void)_y; {at4} }}\n{inc_fn}}};\n")
+    low = Lowerer(ity, params)
+    body = "\n    ".join(low.statements(stmts, "_v"))
+    epi = (f"struct EPI {{ @FIELDS@\n"
+           f"  __device__ void operator()(float _v, {ity} _x) const {{\n"
+           f"    const {ity} _y = 0; const {ity} _global_id = _x; (void)_y; (void)_global_id;\n    {body}\n  }} }};\n")
+    op = 0 if red.op == ReduceOp.SUM else 1
+    init = _init_list(params)
+    fn = "reduce_rows" if mode == "rows" else "reduce_cols"
+    src = ((ld + epi).replace("@FIELDS@", _fields(params)) +
+           f"extern \"C\" __global__ void __launch_bounds__(256) {KNAME}({_params_decl(params)}) {{\n"
+           f"  adhip::{fn}<{op}>(LD{{{init}}}, EPI{{{init}}}, {V}u, {R}u, {'true' if pad_zero else 'false'});\n}}\n")
+    grid = (ceil(V / 4), 1, 1) if mode == "rows" else (ceil(V / 64), 1, 1)
+    return KernelPlan(src, grid, (256, 1, 1), _plan_args(params), family="reduce",
+                      bytes=4 * V * R + 4 * V)
+
+
+# ------------------------------------------------------------------ lockstep fallback
+def lockstep_plans(stmts, n, index_kind, n_cols, init_node, scratch_base):
+    """Exact lockstep semantics for a command with cross-element memory
+    dependences: one kernel per statement, each computing its value for every
+    element into a staging array before a second kernel stores it.  Temps and
+    the DotProd/Reduce value live in scratch arrays.  Returns (plans,
+    scratch floats used)."""
+    temps = [node.id for kind, node in stmts if kind == "tmp"]
+    off = scratch_base
+    temp_off = {}
+    for t in temps:
+        temp_off[t] = off
+        off += n
+    stage_off = off
+    off += n
+    init_off = off
+    off += n
+    plans = []
+    if init_node is not None:
+        sink = _scratch_km(init_off, _identity_access(index_kind, n_cols))
+        fake = _ValueSink(sink)
+        if isinstance(init_node, DotProdNode):
+            plans.append(dotprod_plan([("init", fake)], init_node))
+        else:
+            plans.append(reduce_plan([("init", fake)], init_node))
+    for kind, node in stmts:
+        if kind == "tmp":
+            continue
+        plans.append(_stmt_plan(kind, node, n, index_kind, n_cols, temp_off, stage_off, init_off,
+                                to_stage=True))
+        plans.append(_stmt_plan(kind, node, n, index_kind, n_cols, temp_off, stage_off, init_off,
+                                to_stage=False))
+    return plans, off - scratch_base
+
+
+def _identity_access(index_kind, n_cols):
+    if index_kind == "dp":
+        return Add(Mult(X(), Val(Constant(n_cols))), Y())
+    if index_kind == "red":
+        return X()
+    return Global()
+
+
+class _ValueSink:
+    """A stand-in result node: ``kres`` receives the DotProd/Reduce value."""
+
+    def __init__(self, kres):
+        self.kres = kres
+        self.kargs = []
+
+
+def _stmt_plan(kind, node, n, index_kind, n_cols, temp_off, stage_off, init_off, to_stage):
+    params = Params()
+    bound = max(n, _expr_bound([(kind, node)], max(n - 1, 0), max(n - 1, 0), max(n_cols - 1, 0)))
+    ity = _ity(bound)
+    low = Lowerer(ity, params)
+    # temps and the init value are scratch arrays indexed by element
+    init_p = params.ptr("scratch", 0, init_off)
+
+    def operand(karg, _orig=low.operand):
+        if isinstance(karg, KMatrix) and karg.is_temp:
+            p = params.ptr("scratch", 0, temp_off[karg.id])
+            return f"{p}[_global_id]"
+        if isinstance(karg, KConcat):
+            cond = lower_index(karg.condition, ity)
+            return f"({cond} ? ({operand(karg.karg_two)}) : ({operand(karg.karg_one)}))"
+        return _orig(karg)
+    low.operand = operand
+    stage_p = params.ptr("scratch", 0, stage_off)
+    if to_stage:
+        value = low.rhs(kind, node, f"{init_p}[_global_id]")
+        line = f"{stage_p}[_global_id] = {value};"
+    else:
+        if node.kres.is_temp:
+            p = params.ptr("scratch", 0, temp_off[node.kres.id])
+            line = f"{p}[_global_id] = {stage_p}[_global_id];"
+        else:
+            p, idx, _ = low._loc(node.kres)
+            line = f"{p}[{idx}] = {stage_p}[_global_id];"
+    setup = ""
+    if index_kind == "dp":
+        setup = (f"const {ity} _x = _global_id / ({ity}){n_cols}; "
+                 f"const {ity} _y = _global_id % ({ity}){n_cols}; (void)_x; (void)_y;")
+    elif index_kind == "red":
+        setup = f"const {ity} _x = _global_id; const {ity} _y = 0; (void)_x; (void)_y;"
+    src = f"""extern "C" __global__ void __launch_bounds__({BLOCK}) {KNAME}({_params_decl(params)}, unsigned long long n_) {{
+  const {ity} _global_id = ({ity})blockIdx.x * {BLOCK}u + threadIdx.x;
+  if (_global_id >= ({ity})n_) return;
+  {setup}
+  {line}
+}}
+"""
+    return KernelPlan(src, (max(1, ceil(n / BLOCK)), 1, 1), (BLOCK, 1, 1), _plan_args(params, (n,)),
+                      family="elw")
+
+
+# ------------------------------------------------------------------ per-command entry
+def command_plans(cmd, buffers: BufferInfo, scratch_base: int):
+    """Plans for one Proc command and the scratch floats they need."""
+    if isinstance(cmd, (BinaryNode, UnaryNode, ContigiousNode)):
+        stmts, n, kind, cols, init = statements([cmd]), prod(cmd.shape), "global", 1, None
+    elif isinstance(cmd, ElwFuse):
+        stmts, n, kind, cols, init = statements(cmd.nodes), prod(cmd.init_node.shape), "global", 1, None
+    elif isinstance(cmd, DotProdNode):
+        stmts, n, kind, cols, init = statements([cmd]), prod(cmd.shape), "dp", cmd.shape[1], cmd
+    elif isinstance(cmd, DPElwFuse):
+        dp = cmd.init_node
+        stmts, n, kind, cols, init = statements(cmd.nodes), prod(dp.shape), "dp", dp.shape[1], dp
+    elif isinstance(cmd, ReduceNode):
+        stmts, n, kind, cols, init = statements([cmd]), cmd.children_shapes[0][0], "red", 1, cmd
+    elif isinstance(cmd, ReduceElwFuse):
+        red = cmd.init_node
+        stmts, n, kind, cols, init = statements(cmd.nodes), red.children_shapes[0][0], "red", 1, red
+    else:
+        raise TypeError(f"Encountered unexpected cmd: {cmd}")
+
+    if hazards(stmts, buffers, "xy" if init is not None else "global"):
+        return lockstep_plans(stmts, n, kind, cols, init, scratch_base) + (True,)
+    if isinstance(init, DotProdNode):
+        return [dotprod_plan(stmts, init)], 0, False
+    if isinstance(init, ReduceNode):
+        return [reduce_plan(stmts, init)], 0, False
+    return [elementwise_plan(stmts, n)], 0, False

@@ -1,0 +1,101 @@
+/*
+ * adhip.h -- C ABI of libadhip.so, the MI355X execution backend for the
+ * procedural IR of the `ad` autodiff compiler.
+ *
+ * The reference backend reaches its device through ctypes bindings of the
+ * OpenCL C API (autodiff/device/opencl/cl_helper.py).  Each entry point
+ * below replaces the OpenCL calls named beside it; the Python backend
+ * (ad_amd/device/hip) binds these with ctypes the same way.
+ *
+ * Conventions: every int-returning call returns 0 on success, otherwise a
+ * hipError_t / hiprtcResult value or one of the ADHIP_E_* codes, and the
+ * message is available from adhip_last_error().  One context per process
+ * and thread; all device work of a context is ordered on one HIP stream.
+ * No PyTorch or other framework types cross this boundary.
+ */
+#ifndef ADHIP_H
+#define ADHIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct adhip_ctx adhip_ctx;
+typedef struct adhip_module adhip_module;
+typedef struct adhip_graph adhip_graph;
+
+#define ADHIP_E_ARG      1001  /* bad argument (null pointer, size, range) */
+#define ADHIP_E_STATE    1002  /* call not valid in the current state */
+#define ADHIP_E_COMPILE  1003  /* hipRTC compile failed; log returned */
+#define ADHIP_E_NOTFOUND 1004  /* kernel symbol not found in module */
+
+/* Device + stream + pinned staging.  Replaces clGetPlatformIDs /
+ * clGetDeviceIDs / clCreateContext / clCreateCommandQueue
+ * (cl_helper.py:36-139, device.py:16-51). */
+int  adhip_create(int device, adhip_ctx** out);
+/* Frees everything the context owns.  Replaces clReleaseMemObject /
+ * clReleaseKernel / clReleaseCommandQueue / clReleaseContext
+ * (cl_helper.py:140-175, device.py:139-153). */
+void adhip_destroy(adhip_ctx* ctx);
+/* Message of the last failing call on this context (thread-local when
+ * ctx is NULL). */
+const char* adhip_last_error(adhip_ctx* ctx);
+/* Number of compute units and device name, for launch sizing and logs. */
+int  adhip_device_info(adhip_ctx* ctx, int* num_cu, char* name, size_t name_cap);
+
+/* One hipMalloc holding every buffer of a Proc (the tetris arena, each
+ * Tensor, the hoisted leftovers) plus scratch; zero-filled.  Replaces one
+ * clCreateBuffer per AllocEntry (cl_helper.py:151-170). */
+int  adhip_arena_reserve(adhip_ctx* ctx, size_t bytes, uint64_t* dev_base);
+
+/* Stream-ordered host -> device copy of `bytes` into arena byte offset
+ * `dst_off`.  The host buffer is copied to pinned staging before the call
+ * returns, so it is only borrowed for the call.  Replaces
+ * clEnqueueWriteBuffer (cl_helper.py:304-332). */
+int  adhip_write(adhip_ctx* ctx, uint64_t dst_off, const void* host, size_t bytes);
+/* Blocking device -> host copy after all queued work.  Replaces
+ * clEnqueueReadBuffer with blocking_read (cl_helper.py:262-302). */
+int  adhip_read(adhip_ctx* ctx, uint64_t src_off, void* host, size_t bytes);
+/* Stream-ordered device -> device copy inside the arena (capturable). */
+int  adhip_copy(adhip_ctx* ctx, uint64_t dst_off, uint64_t src_off, size_t bytes);
+
+/* hipRTC compile of a kernel module for the context's device (gfx950).
+ * Thread-safe and context-free so callers may compile in parallel.  The
+ * code object is returned in a malloc'd buffer (free with adhip_free).
+ * Replaces clCreateProgramWithSource + clBuildProgram
+ * (cl_helper.py:357-406). */
+int  adhip_compile(const char* src, const char* options, void** code, size_t* code_size,
+                   char* log, size_t log_cap);
+void adhip_free(void* p);
+/* Load a code object; look up kernels by name.  Replaces clCreateKernel
+ * (cl_helper.py:388-400). */
+int  adhip_module_load(adhip_ctx* ctx, const void* code, size_t code_size, adhip_module** out);
+int  adhip_module_function(adhip_module* mod, const char* name, void** fn);
+
+/* Launch `fn` with a packed argument buffer (every argument one 8-byte
+ * slot: device pointers and int64 values).  Replaces clSetKernelArg +
+ * clEnqueueNDRangeKernel (cl_helper.py:408-455). */
+int  adhip_launch(adhip_ctx* ctx, void* fn, const uint32_t grid[3], const uint32_t block[3],
+                  uint32_t shared_bytes, const uint64_t* args, size_t nargs);
+
+/* Record the context stream's work between begin and end as a HIP graph,
+ * then replay it.  The reference replays a loop body by re-enqueueing
+ * every command from Python (device.py:121-129). */
+int  adhip_graph_begin(adhip_ctx* ctx);
+int  adhip_graph_end(adhip_ctx* ctx, adhip_graph** out);
+int  adhip_graph_launch(adhip_ctx* ctx, adhip_graph* g);
+void adhip_graph_destroy(adhip_graph* g);
+
+/* Wait for all queued work.  Replaces clFinish (cl_helper.py:457-458). */
+int  adhip_sync(adhip_ctx* ctx);
+
+/* Stream events for timing (milliseconds between two recorded events). */
+int  adhip_event_record(adhip_ctx* ctx, int slot);
+int  adhip_event_elapsed(adhip_ctx* ctx, int slot_a, int slot_b, float* ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,158 @@
+"""Static analyses of the HIP code generator, checked by brute force, and
+the C ABI of libadhip.so (loads and exports what include/adhip.h declares;
+no device calls)."""
+import ctypes
+import pathlib
+import re
+
+import numpy as np
+import pytest
+from hypothesis import given, settings
+from hypothesis import strategies as st
+
+from ad_amd.device.hip import analysis, codegen
+from ad_amd.expr import (Add, BitwiseAnd, Constant, Div, Global, MoreThan, Mult, Remainder,
+                         ShiftLeft, ShiftRight, Val, X, Y, evaluate)
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+
+
+def C(v):
+    return Val(Constant(v))
+
+
+@st.composite
+def exprs(draw, depth=3, leaves=(Global,)):
+    if depth == 0 or draw(st.integers(0, 3)) == 0:
+        if draw(st.booleans()):
+            return draw(st.sampled_from(leaves))()
+        return C(draw(st.integers(0, 40)))
+    op = draw(st.sampled_from(["add", "mul", "shl", "shr", "div", "mod", "and", "gt"]))
+    a = draw(exprs(depth - 1, leaves))
+    k = draw(st.integers(1, 12))
+    if op == "add":
+        return Add(a, draw(exprs(depth - 1, leaves)))
+    if op == "mul":
+        return Mult(a, C(k))
+    if op == "shl":
+        return ShiftLeft(a, C(k % 5))
+    if op == "shr":
+        return ShiftRight(a, C(k % 5))
+    if op == "div":
+        return Div(a, C(k))
+    if op == "mod":
+        return Remainder(a, C(k))
+    if op == "and":
+        return BitwiseAnd(a, C(k * 5))
+    return MoreThan(a, C(k))
+
+
+@settings(max_examples=300, deadline=None)
+@given(exprs())
+def test_split_const_preserves_value(e):
+    core, c = analysis.split_const(e)
+    for g in range(64):
+        assert evaluate(core, g=g) + c == evaluate(e, g=g)
+
+
+@settings(max_examples=300, deadline=None)
+@given(exprs())
+def test_upper_bound_is_sound(e):
+    ub = analysis.upper_bound(e, gmax=63)
+    assert max(evaluate(e, g=g) for g in range(64)) <= ub
+
+
+@settings(max_examples=500, deadline=None)
+@given(exprs(depth=4))
+def test_vec_class_is_sound(e):
+    """AFF: f(4t+i) == f(4t)+i (and f(4t) % 4 == 0 when aligned);
+    INV: f(4t+i) == f(4t), over every aligned group."""
+    vc = analysis.vec_class(e, Global)
+    for t in range(0, 256, 4):
+        base = evaluate(e, g=t)
+        for i in range(4):
+            v = evaluate(e, g=t + i)
+            if vc.kind == analysis.AFF:
+                assert v == base + i
+            elif vc.kind == analysis.INV:
+                assert v == base
+        if vc.kind == analysis.AFF and vc.al:
+            assert base % 4 == 0
+        if vc.kind == analysis.INV and vc.al:
+            assert base % 4 == 0
+
+
+@settings(max_examples=300, deadline=None)
+@given(exprs(depth=3, leaves=(X, Y)))
+def test_vec_class_other_axis_is_invariant(e):
+    """Classifying along Y treats X as fixed within a group."""
+    vc = analysis.vec_class(e, Y)
+    for x in (0, 3, 7):
+        for t in range(0, 64, 4):
+            base = evaluate(e, x=x, y=t)
+            for i in range(4):
+                v = evaluate(e, x=x, y=t + i)
+                if vc.kind == analysis.AFF:
+                    assert v == base + i
+                elif vc.kind == analysis.INV:
+                    assert v == base
+
+
+@pytest.mark.parametrize("r", list(range(1, 40)) + [255, 256, 1000, 1024])
+def test_tree_inclusion_matches_simulation(r):
+    """codegen.tree_inclusion == the reference tree (reduce.py:33-43) run on
+    one-hot rows."""
+    L = -(-r // 2) * 2
+    inc = set(codegen.tree_inclusion(r))
+    for y in range(L):
+        s = [0.0] * L
+        s[y] = 1.0
+        off = L // 2
+        while off > 0:
+            for j in range(off):
+                s[j] += s[j + off]
+            off >>= 1
+        assert (s[0] == 1.0) == (y in inc)
+
+
+def test_library_exports_header_symbols():
+    """libadhip.so loads and exports every function include/adhip.h declares."""
+    header = (ROOT / "include" / "adhip.h").read_text()
+    names = set(re.findall(r"\b(adhip_[a-z_]+)\s*\(", header))
+    lib = ctypes.CDLL(str(ROOT / "ad_amd" / "device" / "hip" / "libadhip.so"))
+    missing = [n for n in sorted(names) if not hasattr(lib, n)]
+    assert not missing, missing
+    from ad_amd.device.hip import runtime
+    assert names == set(runtime.EXPORTS)
+
+
+def test_generated_kernels_compile_for_gfx950():
+    """Every kernel of the MLP and LayerNorm programs compiles through
+    hipRTC for gfx950 (no device needed)."""
+    import ad_amd as ad
+    from ad_amd.alloc import AllocEntry
+    from ad_amd.fusion import FuseBase
+    from ad_amd.graph import Feeder, ForNode, Receiver
+    from ad_amd.node import Node
+    from ad_amd.device.hip.runtime import HEADER_PATH, compile_source
+    from . import programs
+    programs.mlp(steps=1)
+    proc = ad.compile_proc()
+    allocs, cmds = [], []
+
+    def walk(p):
+        for c in p.procedure:
+            if isinstance(c, ForNode):
+                walk(c.get_proc())
+            elif isinstance(c, AllocEntry):
+                allocs.append(c)
+            elif isinstance(c, (Node, FuseBase)) and not isinstance(c, (Feeder, Receiver)):
+                cmds.append(c)
+    walk(proc)
+    info = codegen.BufferInfo()
+    for a in allocs:
+        info.size[a.id] = a.size
+    header = pathlib.Path(HEADER_PATH).read_text()
+    for c in cmds:
+        for plan in codegen.command_plans(c, info, 0)[0]:
+            assert len(compile_source(header + plan.source)) > 0

@@ -1,0 +1,274 @@
+"""The restated compiler front end against the reference's own goldens.
+
+* README.md:177-216 lists the Proc of examples/linear.py (command order,
+  fusion groups, fuse ids, node ids); the restatement must produce it.
+* README.md:21-22 and the 1-layer run in Success.png give the tetris arena
+  totals (11238 of 36758 and 2228 of 4738 floats) and 91 kernels.
+* kernalize + simplify: every access expression equals numpy's index map.
+"""
+import numpy as np
+import pytest
+from hypothesis import given, settings
+from hypothesis import strategies as st
+
+import ad_amd as ad
+from ad_amd.alloc import AllocEntry, DeallocEntry
+from ad_amd.alloc import tetris_opt
+from ad_amd.expr import evaluate
+from ad_amd.fusion import DPElwFuse, ElwFuse, FuseBase, ReduceElwFuse
+from ad_amd.graph import DotProdNode, Feeder, ForNode, Receiver, Tensor
+from ad_amd.nn import SGD, Linear, Sequential, Sigmoid, TransformerEncoder
+
+
+def _mlp_program():
+    net = Sequential(Linear(255, 255), Sigmoid(), Linear(255, 255))
+    opt = SGD(net.parameters(), lr=0.01)
+
+    def f():
+        opt.zero_grad()
+        val = Feeder(lambda: np.full((2, 255), 0.2, dtype=np.float32), shape=[2, 255])
+        net(val).backward()
+        opt.step()
+    ad.ir_for(range(0, 1000), f)
+    Receiver(lambda *a: None, opt.parameters, name="saving params")
+    return ad.compile_proc()
+
+
+def _signature(cmd):
+    """(kind, fuse id or None, [result ids of member nodes])."""
+    if isinstance(cmd, FuseBase):
+        members = [n for n in cmd.nodes if not isinstance(n, (AllocEntry, DeallocEntry))]
+        return (type(cmd).__name__, cmd.fuse_id, [getattr(n, "_orig_id", n.id) for n in members])
+    return (type(cmd).__name__, None, [cmd.id])
+
+
+def test_readme_linear_listing():
+    """README.md:177-216 (examples/linear.py), ids before arena renaming."""
+    proc = _mlp_program()
+    loop = [c for c in proc.procedure if isinstance(c, ForNode)][0]
+    body = [c for c in loop.get_proc().procedure if not isinstance(c, (AllocEntry, DeallocEntry))]
+    kinds = [(type(c).__name__, getattr(c, "fuse_id", None)) for c in body]
+    assert kinds == [("DotProdNode", None), ("ReduceElwFuse", 98), ("Feeder", None), ("DPElwFuse", 94),
+                     ("DPElwFuse", 96), ("ReduceElwFuse", 99), ("DPElwFuse", 95)]
+    groups = {c.fuse_id: [n for n in c.nodes if not isinstance(n, (AllocEntry, DeallocEntry))]
+              for c in body if isinstance(c, FuseBase)}
+    # result ids are renamed by in-place/arena passes; compare operation
+    # kinds and the in-place targets, which keep the README ids
+    assert [type(n).__name__ for n in groups[94]] == ["DotProdNode"] + ["BinaryNode", "BinaryNode", "UnaryNode",
+                                                                         "BinaryNode", "UnaryNode", "BinaryNode",
+                                                                         "UnaryNode", "BinaryNode", "BinaryNode",
+                                                                         "BinaryNode", "BinaryNode", "BinaryNode"]
+    assert [n.kres.id for n in groups[96]][-1] == 0
+    assert [n.kres.id for n in groups[99]][-1] == 1
+    assert [n.kres.id for n in groups[95]][-1] == 2
+    assert [n.kres.id for n in groups[98]][-1] == 3
+    temps = {n.kres.id for g in groups.values() for n in g if n.kres.is_temp}
+    assert {5, 8, 81, 13, 15, 30, 31, 33, 34, 36, 37, 45, 77, 47, 83, 27, 87, 51, 89} <= temps
+    recv = [c for c in proc.procedure if isinstance(c, Receiver)][0]
+    assert recv.id == 75 and [k.id for k in recv.kargs] == [0, 1, 2, 3]
+    feeder = body[2]
+    assert feeder.kres.offset is None and repr(feeder.kres.access) == "(Global + 510)"
+
+
+def _transformer_program(layers):
+    net = TransformerEncoder(num_layers=layers, d_model=64, num_heads=4, ff_dim=128)
+    opt = SGD(net.parameters(), lr=0.01)
+
+    def f():
+        opt.zero_grad()
+        val = Feeder(lambda: np.full((2, 64), 0.3, dtype=np.float32), shape=[2, 64])
+        net(val).backward()
+        opt.step()
+    ad.ir_for(range(0, 500), f)
+    Receiver(lambda *a: None, opt.parameters, name="saving params")
+    return ad.compile_proc()
+
+
+def test_readme_transformer_arena_total():
+    """README.md:21-22: 'ALLOC DEBUG: Using: 11238 out of 36758'."""
+    _transformer_program(6)
+    assert (tetris_opt.stats["used"], tetris_opt.stats["total"]) == (11238, 36758)
+
+
+def test_one_layer_arena_total_and_kernel_count():
+    """Success.png (1-layer run): 2228 of 4738 floats, 91 kernels."""
+    proc = _transformer_program(1)
+    assert (tetris_opt.stats["used"], tetris_opt.stats["total"]) == (2228, 4738)
+    loop = [c for c in proc.procedure if isinstance(c, ForNode)][0]
+    kernels = [c for c in loop.get_proc().procedure
+               if not isinstance(c, (AllocEntry, DeallocEntry, Feeder, Receiver))]
+    assert len(kernels) == 91
+
+
+def test_tetris_no_live_overlap():
+    """No two variables that are live at the same time share arena floats."""
+    _transformer_program(2)
+    from ad_amd.alloc.tetris_opt import VarEntry  # noqa: F401
+    # re-run the placement on a synthetic lifetime set
+    from ad_amd.alloc.tetris_opt import place
+    rng = np.random.default_rng(0)
+    for _ in range(50):
+        entries = []
+        for i in range(30):
+            s = int(rng.integers(0, 100))
+            entries.append(VarEntry(i, s, s + int(rng.integers(1, 20)), int(rng.integers(1, 50))))
+        entries.sort(key=lambda e: -e.size)
+        high = place(entries)
+        assert high <= sum(e.size for e in entries)
+        for a in entries:
+            for b in entries:
+                if a is b:
+                    continue
+                live = max(a.start_idx, b.start_idx) < min(a.end_idx, b.end_idx)
+                mem = a.offset < b.offset + b.size and b.offset < a.offset + a.size
+                assert not (live and mem)
+
+
+# ---------------------------------------------------------------- indexing
+def _apply(kind, arg, node, idx):
+    """Apply one data-movement op to the graph node and to a numpy array of
+    source indices."""
+    if kind == "permute":
+        return node.permute(arg), np.transpose(idx, arg)
+    if kind == "view":
+        return node.view(list(arg)), idx.reshape(arg)
+    if kind == "broadcast":
+        d, size = arg
+        return node.broadcast(d, size), np.broadcast_to(idx, idx.shape[:d] + (size,) + idx.shape[d + 1:])
+    if kind == "index":
+        d, s, e = arg
+        sl = [slice(None)] * idx.ndim
+        sl[d] = slice(s, e)
+        return node[tuple(sl)] if d == 0 else _index(node, d, s, e), idx[tuple(sl)]
+    raise ValueError(kind)
+
+
+def _index(node, d, s, e):
+    from ad_amd.graph import IndexNode
+    return IndexNode(node, s, e, d)
+
+
+@st.composite
+def chains(draw):
+    shape = draw(st.lists(st.integers(1, 5), min_size=1, max_size=3))
+    ops = []
+    cur = list(shape)
+    for _ in range(draw(st.integers(0, 4))):
+        kind = draw(st.sampled_from(["permute", "view", "broadcast", "index"]))
+        if kind == "permute" and len(cur) > 1:
+            # the reference only builds involutions (T, mT, the reduce swap);
+            # for others its index map is wrong, see test_permute_non_involution
+            i, j = draw(st.integers(0, len(cur) - 1)), draw(st.integers(0, len(cur) - 1))
+            perm = list(range(len(cur)))
+            perm[i], perm[j] = perm[j], perm[i]
+            ops.append((kind, list(perm)))
+            cur = [cur[p] for p in perm]
+        elif kind == "view":
+            n = int(np.prod(cur))
+            divs = [d for d in range(1, n + 1) if n % d == 0]
+            a = draw(st.sampled_from(divs))
+            new = [a, n // a] if draw(st.booleans()) else [n]
+            ops.append((kind, tuple(new)))
+            cur = new
+        elif kind == "broadcast" and 1 in cur:
+            d = cur.index(1)
+            size = draw(st.integers(2, 4))
+            ops.append((kind, (d, size)))
+            cur = cur[:d] + [size] + cur[d + 1:]
+        elif kind == "index":
+            d = draw(st.integers(0, len(cur) - 1))
+            if cur[d] > 1:
+                s = draw(st.integers(0, cur[d] - 1))
+                e = draw(st.integers(s + 1, cur[d]))
+                ops.append((kind, (d, s, e)))
+                cur = cur[:d] + [e - s] + cur[d + 1:]
+    return shape, ops
+
+
+def _raw_access(node, shape_out):
+    """The unsimplified access of an elementwise consumer of ``node``:
+    peel the data-movement chain and map Global back to the source
+    (kernalize.py:199-242 without simplify_expr)."""
+    from copy import deepcopy
+    from ad_amd.expr import Global
+    from ad_amd.graph import BroadcastNode, IndexNode, PermuteNode, ViewNode
+    from ad_amd.helper import global_to_ndim, ndim_change_datacmds, ndim_to_global
+    cmds = []
+    while isinstance(node, (PermuteNode, ViewNode, BroadcastNode, IndexNode)):
+        cmds.append(node)
+        node = node.child
+    dim = ndim_change_datacmds(global_to_ndim(Global(), list(shape_out)), cmds)
+    return ndim_to_global(dim, node.shape), node
+
+
+def _build_chain(case):
+    shape, ops = case
+    src = Tensor(np.zeros(shape, dtype=np.float32))
+    node, idx = src, np.arange(int(np.prod(shape))).reshape(shape)
+    for kind, arg in ops:
+        node, idx = _apply(kind, arg, node, idx)
+    return src, node, idx
+
+
+@settings(max_examples=200, deadline=None)
+@given(chains())
+def test_index_map_matches_numpy(case):
+    """ndim_change_datacmds / global_to_ndim / ndim_to_global
+    (helper.py:19-73): the unsimplified access of any chain of permutes
+    (involutions), views, broadcasts and slices addresses exactly the
+    element numpy's view semantics select."""
+    ad.reset()
+    src, node, idx = _build_chain(case)
+    raw, source = _raw_access(node, node.shape)
+    assert source is src
+    flat = idx.reshape(-1)
+    assert [evaluate(raw, g=g) for g in range(flat.size)] == flat.tolist()
+
+
+@settings(max_examples=200, deadline=None)
+@given(chains())
+def test_simplify_without_size_preserves_value(case):
+    """simplify_expr(e, None) (simplify.py:6-166): the size-free rules keep
+    the value of every access the front end builds."""
+    from copy import deepcopy
+    from ad_amd.expr.simplify import simplify_expr
+    ad.reset()
+    src, node, idx = _build_chain(case)
+    raw, _ = _raw_access(node, node.shape)
+    want = [evaluate(raw, g=g) for g in range(idx.size)]
+    simp = simplify_expr(deepcopy(raw), None)
+    assert [evaluate(simp, g=g) for g in range(idx.size)] == want
+
+
+def test_size_rule_applies_below_top_level():
+    """simplify.py:129-133 drops ``& (size-1)`` from ANY subexpression of an
+    elementwise access of ``size`` elements, including ones whose value can
+    exceed size-1.  Slicing rows 1..3 of a [4] view of a [2,2] view of a
+    [1,4] tensor therefore reads elements [1, 0] instead of [1, 2]; the
+    restatement keeps the reference's expression (parity over intent)."""
+    src = Tensor(np.zeros((1, 4), dtype=np.float32))
+    out = src.view([2, 2]).view([4])[1:3].contigious()
+    Receiver(lambda *a: None, [out])
+    proc = ad.compile_proc()
+    cmd = [c for c in proc.procedure if type(c).__name__ == "ContigiousNode"][0]
+    assert [evaluate(cmd.kargs[0].access, g=g) for g in range(2)] == [1, 0]
+
+
+def test_permute_non_involution_follows_reference():
+    """helper.py:55-59 maps a permute with ``new_dim[i] = dim[perm[i]]``,
+    which is the index map of the INVERSE permutation.  For the involutions
+    the reference builds this is exact; for a 3-cycle on a cube it reads the
+    element of ``transpose(x, inverse(perm))`` -- the reference's behaviour,
+    kept for parity."""
+    shape = [3, 3, 3]
+    perm = [1, 2, 0]
+    inv = [perm.index(i) for i in range(3)]
+    src = Tensor(np.zeros(shape, dtype=np.float32))
+    out = src.permute(perm).contigious()
+    Receiver(lambda *a: None, [out])
+    proc = ad.compile_proc()
+    cmd = [c for c in proc.procedure if type(c).__name__ == "ContigiousNode"][0]
+    idx = np.arange(27).reshape(shape)
+    got = [evaluate(cmd.kargs[0].access, g=g) for g in range(27)]
+    assert got == np.transpose(idx, inv).reshape(-1).tolist()
+    assert got != np.transpose(idx, perm).reshape(-1).tolist()

@@ -1,0 +1,136 @@
+"""Parity of the HIP backend with the CPU oracle on identical programs.
+
+Tolerances: data movement and +,* chains are bit-exact; anything through a
+dot product or reduction (reassociated on the GPU) or a libm function
+(exp2/log2/sin differ by ulps between glibc and the ROCm device library) is
+checked at rtol 1e-4 / atol 1e-5 per step."""
+import pathlib
+
+import numpy as np
+import pytest
+
+import ad_amd as ad
+from ad_amd.graph import Receiver, Tensor
+from oracle import OracleDevice
+
+from . import programs
+
+GOLDEN = pathlib.Path(__file__).parent / "golden"
+
+pytestmark = pytest.mark.gpu
+
+
+def run_both(build, hip):
+    ad.reset()
+    out_hip = build()
+    ad.execute(device=hip())
+    ad.reset()
+    out_cpu = build()
+    ad.execute(device=OracleDevice())
+    return out_hip, out_cpu
+
+
+def assert_params_close(a, b, rtol=1e-4, atol=1e-5):
+    assert len(a["params"]) == len(b["params"])
+    for x, y in zip(a["params"], b["params"]):
+        np.testing.assert_allclose(x, y, rtol=rtol, atol=atol)
+
+
+@pytest.mark.parametrize("M,K,N", [(2, 255, 255), (128, 64, 128), (130, 70, 257), (256, 512, 64), (1, 3, 1)])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+def test_dotprod_shapes(hip, M, K, N, ta, tb):
+    """A @ B through the MFMA template for row-major and transposed
+    operands, against float64 numpy with a K-scaled bound."""
+    rng = np.random.default_rng(M * 7 + K * 3 + N)
+    a = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    b = rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    A = Tensor(a)
+    B = Tensor(b)
+    r = (A.T() if ta else A) @ (B.T() if tb else B)
+    got = {}
+    Receiver(lambda v: got.setdefault("r", v.copy()), [r])
+    ad.execute(device=hip())
+    ref = (a.T if ta else a).astype(np.float64) @ (b.T if tb else b).astype(np.float64)
+    bound = 4 * K * np.finfo(np.float32).eps * (np.abs(a).max() * np.abs(b).max()) + 1e-6
+    np.testing.assert_allclose(got["r"], ref, rtol=0, atol=bound)
+
+
+def test_reference_known_answers_dotprod(hip):
+    """tests/dotprod_test.py:8-9 of the reference (torch seed 42 inputs)."""
+    d = np.load(GOLDEN / "dotprod_test_inputs.npz")
+    inp = Tensor(d["inp"], requires_grad=True)
+    w = Tensor(d["weight"], requires_grad=True)
+    b = Tensor(d["bias"], requires_grad=True)
+    r = (inp @ w) + b
+    r.backward()
+    got = {}
+    Receiver(lambda res, g: got.update(r=res.copy(), g=g.copy()), [r, inp.grad()])
+    ad.execute(device=hip())
+    assert round(float(got["r"].sum()), 4) == -3.2747
+    assert round(float(got["g"].sum()), 4) == 8.2885
+
+
+def test_reference_known_answers_unary(hip):
+    """tests/unary_test.py:11-14 of the reference."""
+    inp = Tensor(np.array([[0.3, 0.2, 0.7, 0.54], [0.13, 0.77, 0.23, 0.22]]), requires_grad=True)
+    result = inp.exp2() + 3
+    result = result.sqrt().recip() * -2.5 + result.log2()
+    result = result.sin()
+    result_two = (inp > 0.5) * inp.exp2()
+    result.backward()
+    result_two.backward()
+    got = {}
+    Receiver(lambda a, b, c: got.update(a=a.copy(), b=b.copy(), c=c.copy()), [result, result_two, inp.grad()])
+    ad.execute(device=hip())
+    assert round(float(got["a"].sum()), 5) == 6.2689
+    assert round(float(got["b"].sum()), 5) == 4.78375
+    assert round(float(got["c"].sum()), 5) == 5.39896
+
+
+def test_reference_known_answers_layernorm(hip):
+    """tests/layernorm_test.py:19-22 of the reference; exercises the
+    lockstep path (the output reuses the arena slot of 1/sqrt(var))."""
+    from ad_amd.nn import LayerNorm
+    x = Tensor(np.array([[5.0, 6.0, 3.0], [4.0, 5.0, 6.0]]), requires_grad=True)
+    ln = LayerNorm(3)
+    res = ln(x)
+    res.backward()
+    got = {}
+    Receiver(lambda a, b, c: got.update(y=a.copy(), db=b.copy(), ds=c.copy()),
+             [res, ln.bias.grad().contigious(), ln.scale.grad().contigious()])
+    ad.execute(device=hip())
+    assert round(float(got["y"].flatten()[0]), 4) == 0.2673
+    assert round(float(got["db"].flatten()[0]), 4) == 2.0
+    assert round(float(got["ds"].flatten()[0]), 4) == -0.9575
+
+
+def test_reference_known_answers_concat_pow2(hip):
+    """tests/concat_test.py:28-34 and powtwo_test.py:18-27: exact values."""
+    x = Tensor(np.array([[5.0, 6.0, 3.0, 1.0], [4.0, 5.0, 6.0, 3.0]]), requires_grad=True)
+    y = Tensor(np.array([[8.0, 9.0, 3.0, 6.0], [3.0, 5.0, 4.0, 2.0]]), requires_grad=True)
+    res = ad.concat([x * 2, y * 3], 1).contigious()
+    res.backward()
+    sq = x.pow2()
+    got = {}
+    Receiver(lambda r, xg, yg, s: got.update(r=r.copy(), xg=xg.copy(), yg=yg.copy(), s=s.copy()),
+             [res, x.grad(), y.grad(), sq])
+    ad.execute(device=hip())
+    assert np.array_equal(got["r"], np.array([[10, 12, 6, 2, 24, 27, 9, 18], [8, 10, 12, 6, 9, 15, 12, 6]]))
+    assert got["xg"].sum() == 16 and got["yg"].sum() == 24
+    assert np.array_equal(got["s"], np.array([[25, 36, 9, 1], [16, 25, 36, 9]]))
+
+
+def test_mlp_parity(hip):
+    """examples/linear.py (config 1) for 3 SGD steps: every parameter."""
+    a, b = run_both(lambda: programs.mlp(steps=3), hip)
+    assert_params_close(a, b)
+
+
+def test_layernorm_training_parity(hip):
+    a, b = run_both(lambda: programs.layernorm_step(rows=8, cols=16, steps=3), hip)
+    assert_params_close(a, b)
+
+
+def test_transformer_parity(hip):
+    a, b = run_both(lambda: programs.transformer(layers=1, d_model=32, heads=4, ff=64, seq=4, steps=2), hip)
+    assert_params_close(a, b)
