@@ -10,6 +10,8 @@ All Procs share one arena id; each access to a packed buffer becomes
 from dataclasses import dataclass
 from typing import Dict, List, Optional
 
+import numpy as np
+
 from ..context import context
 from ..expr import Add, Constant, Val
 from ..expr.simplify import simplify_expr
@@ -38,7 +40,48 @@ def _ranges_intersect(r1, r2) -> bool:
 
 def place(entries: List[VarEntry]) -> int:
     """Assign ``offset`` to each entry (already sorted largest first);
-    return the arena high-water mark."""
+    return the arena high-water mark.
+
+    For each entry: the ranges of already placed entries whose lifetimes
+    overlap it, stably sorted by start, intersecting neighbours merged; the
+    entry goes into the last gap between consecutive ranges that is wide
+    enough, else at the end of the last range, else at 0.  The lifetime
+    query runs vectorised over all placed entries."""
+    n = len(entries)
+    starts = np.fromiter((e.start_idx for e in entries), dtype=np.int64, count=n)
+    ends = np.fromiter((e.end_idx for e in entries), dtype=np.int64, count=n)
+    sizes = np.fromiter((e.size for e in entries), dtype=np.int64, count=n)
+    offsets = np.zeros(n, dtype=np.int64)
+    high = 0
+    for i, entry in enumerate(entries):
+        live = np.nonzero(np.maximum(starts[:i], starts[i]) < np.minimum(ends[:i], ends[i]))[0]
+        lo = offsets[live]
+        order = np.argsort(lo, kind="stable")     # Python's stable sort by start
+        taken = list(zip(lo[order].tolist(), (lo[order] + sizes[live][order]).tolist()))
+        j = 0
+        while j < len(taken) - 1:
+            if _ranges_intersect(taken[j], taken[j + 1]):
+                merged = (min(taken[j][0], taken[j + 1][0]), max(taken[j][1], taken[j + 1][1]))
+                del taken[j]
+                del taken[j]
+                taken.insert(j, merged)
+            else:
+                j += 1
+        offset = -1
+        for t in range(len(taken) - 1):
+            if taken[t + 1][0] - taken[t][1] >= entry.size:
+                offset = taken[t][1]
+        if offset == -1:
+            offset = taken[-1][-1] if len(taken) > 0 else 0
+        entry.offset = offset
+        offsets[i] = offset
+        high = max(high, offset + entry.size)
+    return high
+
+
+def place_reference(entries: List[VarEntry]) -> int:
+    """Direct restatement of the placement loop (tetris_opt.py:108-149), one
+    lifetime check per placed entry; kept as the check of ``place``."""
     placed: List[VarEntry] = []
     high = 0
     for entry in entries:
@@ -98,42 +141,40 @@ def tetris_opt(proc):
     temp_id = context.get_id()
     stats["used"], stats["total"] = max_temp_size, total_size
 
+    # One pass: the reference loops over every packed variable for every
+    # operand; after its rename an operand carries ``temp_id``, which matches
+    # no variable, so a single lookup per operand gives the same result.
+    by_var = {proc_id: {e.var_id: e for e in entries} for proc_id, entries in offsetted.items()}
+
+    def relabel(karg, table):
+        from ..kernalize import KConcat, KMatrix
+        if isinstance(karg, KMatrix):
+            entry = table.get(karg.id)
+            if entry is not None:
+                karg.tetris_var = (entry.var_id, entry.offset, entry.size)
+                karg.rename(entry.var_id, temp_id, _add_offset(entry.offset))
+        elif isinstance(karg, KConcat):
+            relabel(karg.karg_one, table)
+            relabel(karg.karg_two, table)
+
     def replace_to_temp(node, proc_id):
-        if proc_id not in offsetted:
+        table = by_var.get(proc_id)
+        if table is None:
             return node
-        entries = offsetted[proc_id]
         if isinstance(node, (AllocEntry, DeallocEntry)):
-            for entry in entries:
-                if entry.var_id == node.id:
-                    return None
+            return None if node.id in table else node
         if not isinstance(node, Node):
             return node
-        for idx in range(len(node.kargs)):
-            for entry in entries:
-                _tag(node.kargs[idx], entry)
-                node.kargs[idx].rename(entry.var_id, temp_id, _add_offset(entry.offset))
-        for entry in entries:
-            if not node.kres.is_none():
-                _tag(node.kres, entry)
-                node.kres.rename(entry.var_id, temp_id, _add_offset(entry.offset))
+        for karg in node.kargs:
+            relabel(karg, table)
+        if not node.kres.is_none():
+            relabel(node.kres, table)
         return node
     proc.walk(replace_to_temp)
 
     if max_temp_size > 0:
         proc.insert(0, AllocEntry(temp_id, max_temp_size, content=None))
         proc.append(DeallocEntry(temp_id, max_temp_size))
-
-
-def _tag(karg, entry):
-    """Remember which packed variable (id, offset, size) an operand addresses,
-    for the backend's aliasing checks.  Does not change the IR."""
-    from ..kernalize import KConcat, KMatrix
-    if isinstance(karg, KMatrix):
-        if karg.id == entry.var_id:
-            karg.tetris_var = (entry.var_id, entry.offset, entry.size)
-    elif isinstance(karg, KConcat):
-        _tag(karg.karg_one, entry)
-        _tag(karg.karg_two, entry)
 
 
 def _add_offset(offset):

@@ -19,6 +19,7 @@ one per statement, each staging its result before storing it
 """
 import hashlib
 import math
+import re
 from dataclasses import dataclass, field
 from math import ceil, prod
 from typing import Dict, List, Optional, Tuple
@@ -33,6 +34,7 @@ from ...kernalize import KConcat, KConstant, KMatrix
 from .analysis import AFF, INV, const_of, split_const, upper_bound, vec_class
 
 BLOCK = 256
+_TEMP_RE = re.compile(r"\btemp_\d+\b")
 
 _OPS = {Add: "+", Minus: "-", Mult: "*", Div: "/", Remainder: "%", ShiftRight: ">>",
         ShiftLeft: "<<", BitwiseAnd: "&", MoreThan: ">", LessThan: "<"}
@@ -41,7 +43,7 @@ _OPS = {Add: "+", Minus: "-", Mult: "*", Div: "/", Remainder: "%", ShiftRight: "
 # ------------------------------------------------------------------ plans
 @dataclass
 class KernelPlan:
-    source: str                   # full source; kernel is named KNAME
+    source: str                   # full source; the kernel symbol is ``name``
     grid: Tuple[int, int, int]
     block: Tuple[int, int, int]
     args: List[tuple]             # ("buf", buffer_id, float_offset) | ("scratch", float_offset) | ("int", v)
@@ -50,9 +52,22 @@ class KernelPlan:
     flops: int = 0                # algorithmic flops (dotprod) for reporting
     bytes: int = 0                # algorithmic bytes for reporting
 
+    name: str = ""                # kernel symbol: adhip_<family>_<hash of the source>
+
+    def __post_init__(self):
+        # register temps are named after node ids; number them by first use
+        # so commands that differ only in ids share one compiled kernel
+        names = {}
+        self.source = _TEMP_RE.sub(lambda m: names.setdefault(m.group(0), f"t{len(names)}_"), self.source)
+        # every template emits the symbol KNAME; give each distinct source its
+        # own symbol so profiles tell kernels apart
+        tag = {"dotprod": "dp", "reduce": "red", "elw": "elw", "copy": "copy"}.get(self.family, "k")
+        self.name = f"adhip_{tag}_{hashlib.sha1(self.source.encode()).hexdigest()[:12]}"
+        self.source = self.source.replace(KNAME, self.name)
+
     @property
     def key(self):
-        return hashlib.sha1(self.source.encode()).hexdigest()[:20]
+        return self.name
 
 
 # ------------------------------------------------------------------ statements
@@ -98,39 +113,78 @@ def _region(km: KMatrix, buffers: BufferInfo):
     return (km.id, 0, buffers.size.get(km.id, 1 << 62)), ("buf", km.id)
 
 
-def _same_map(a: KMatrix, b: KMatrix) -> bool:
-    return a.id == b.id and repr(a.access) == repr(b.access)
+def _unval(e):
+    while type(e) is Val:
+        e = e.v
+    return e
 
 
-def hazards(stmts, buffers: BufferInfo, index_kind: str) -> bool:
-    """True when some element of the command may read or write a location
-    that another element writes (cross-element dependence through memory).
+def _loc_sig(km: KMatrix, index_kind: str, n_cols: int):
+    """Location of an access as a function of the element index ``g``:
+    ``("g", c)`` when it is ``g + c`` (then distinct elements touch distinct
+    locations), otherwise ``("e", text, c)``.  Elements are ``Global`` for
+    elementwise commands, ``X * n_cols + Y`` for a DotProd and ``X`` for a
+    Reduce."""
+    core, c = split_const(km.access)
+    core = _unval(core)
+    if isinstance(core, Global):
+        return ("g", c)
+    if index_kind == "red" and isinstance(core, X):
+        return ("g", c)
+    if index_kind == "dp" and type(core) is Add:
+        a, b = _unval(core.a), _unval(core.b)
+        if isinstance(a, Y):
+            a, b = b, a
+        if isinstance(b, Y):
+            if n_cols == 1 and isinstance(a, X):
+                return ("g", c)
+            if type(a) in (ShiftLeft, Mult) and isinstance(_unval(a.a), X):
+                k = const_of(a.b)
+                if k is not None and (1 << int(k) if type(a) is ShiftLeft else int(k)) == n_cols:
+                    return ("g", c)
+    return ("e", repr(core), c)
 
-    Two accesses on disjoint regions never conflict; two accesses to the same
-    location expression of the same variable touch the same element.  A
-    DotProd/Reduce operand is read for whole rows/columns, so any write
-    overlapping it is a conflict."""
+
+def conflict_pairs(stmts, buffers: BufferInfo, index_kind: str, n_cols: int = 1):
+    """Pairs ``(i, j)``, ``i <= j``, of statement indices that must not run
+    in the same pass over the elements: some element's access in one may
+    touch a location that another element accesses in the other, with at
+    least one of them a write.  Under the reference's statement-by-statement
+    semantics, ``i`` must then finish for every element before ``j`` starts
+    (``i == j``: the statement's reads must all precede its writes).
+
+    Accesses on disjoint regions never conflict; two accesses whose location
+    is ``g + c`` with the same ``c`` touch, for every element, a location no
+    other element touches.  A DotProd/Reduce operand is read for whole
+    rows/columns, so any write overlapping it conflicts."""
     reads, writes = [], []
-    for kind, n in stmts:
-        if kind == "tmp":
+    for si, (kind, n) in enumerate(stmts):
+        if kind in ("tmp", "load", "store"):
             continue
         whole = kind == "init"
         for k in n.kargs:
             for km in _iter_kmatrix(k):
                 if not km.is_temp:
-                    reads.append((km, whole))
+                    reads.append((km, whole, si))
         if not n.kres.is_none() and not n.kres.is_temp:
-            writes.append((n.kres, kind == "init" and index_kind == "xy"))
-    for w, _ in writes:
-        wr, wv = _region(w, buffers)
-        for r, whole in reads + [(x, False) for x, _ in writes if x is not w]:
-            rr, rv = _region(r, buffers)
+            writes.append((n.kres, False, si))
+    out = set()
+    for w, _, wi in writes:
+        wr, _ = _region(w, buffers)
+        wsig = _loc_sig(w, index_kind, n_cols)
+        for r, whole, ri in reads + [(x, False, xi) for x, _, xi in writes if x is not w]:
+            rr, _ = _region(r, buffers)
             if rr[0] != wr[0] or rr[2] <= wr[1] or wr[2] <= rr[1]:
                 continue
-            if not whole and wv == rv and _same_map(w, r):
+            if not whole and wsig[0] == "g" and _loc_sig(r, index_kind, n_cols) == wsig:
                 continue
-            return True
-    return False
+            out.add((min(wi, ri), max(wi, ri)))
+    return sorted(out)
+
+
+def hazards(stmts, buffers: BufferInfo, index_kind: str, n_cols: int = 1) -> bool:
+    """True when the command needs more than one pass over its elements."""
+    return len(conflict_pairs(stmts, buffers, index_kind, n_cols)) > 0
 
 
 # ------------------------------------------------------------------ lowering helpers
@@ -244,6 +298,14 @@ class Lowerer:
             if kind == "tmp":
                 lines.append(f"float temp_{n.id} = 0.0f;")
                 continue
+            if kind == "load":          # temp carried in from an earlier pass
+                tid, off = n
+                lines.append(f"float temp_{tid} = {self.params.ptr('scratch', 0, off)}[_global_id];")
+                continue
+            if kind == "store":         # temp carried out to a later pass
+                tid, off = n
+                lines.append(f"{self.params.ptr('scratch', 0, off)}[_global_id] = temp_{tid};")
+                continue
             value = self.rhs(kind, n, init_value)
             if n.kres.is_temp:
                 lines.append(f"temp_{n.kres.id} = {value};")
@@ -264,7 +326,7 @@ def _ity(bound) -> str:
 def _expr_bound(stmts, gmax, xmax, ymax):
     b = max(gmax, xmax, ymax, 1)
     for kind, n in stmts:
-        if kind == "tmp":
+        if kind in ("tmp", "load", "store"):
             continue
         ks = list(n.kargs) + ([n.kres] if not n.kres.is_none() else [])
         for k in ks:
@@ -298,7 +360,7 @@ def _vector_plan(stmts, n):
     if n % 4 != 0:
         return False
     for kind, node in stmts:
-        if kind == "tmp":
+        if kind in ("tmp", "load", "store"):
             continue
         ks = list(node.kargs) + [node.kres]
         for k in ks:
@@ -417,6 +479,17 @@ def _vector_source(stmts, ity, params: Params) -> str:
         if kind == "tmp":
             temps.append(n.id)
             lines.append(f"float temp_{n.id}[4] = {{0.0f, 0.0f, 0.0f, 0.0f}};")
+            continue
+        if kind == "load":
+            tid, off = n
+            v = fresh("v")
+            lines.append(f"const float4 {v} = *reinterpret_cast<const float4*>({params.ptr('scratch', 0, off)} + _global_id);")
+            lines.append(f"float temp_{tid}[4] = {{{v}.x, {v}.y, {v}.z, {v}.w}};")
+            continue
+        if kind == "store":
+            tid, off = n
+            lines.append(f"*reinterpret_cast<float4*>({params.ptr('scratch', 0, off)} + _global_id) = "
+                         f"make_float4(temp_{tid}[0], temp_{tid}[1], temp_{tid}[2], temp_{tid}[3]);")
             continue
         # operands are loaded before the statement computes (program order)
         for k in n.kargs:
@@ -706,10 +779,104 @@ def command_plans(cmd, buffers: BufferInfo, scratch_base: int):
     else:
         raise TypeError(f"Encountered unexpected cmd: {cmd}")
 
-    if hazards(stmts, buffers, "xy" if init is not None else "global"):
+    pairs = conflict_pairs(stmts, buffers, kind, cols)
+    if not pairs:
+        return single_pass_plans(stmts, n, init), 0, False
+    if any(i == j for i, j in pairs):
         return lockstep_plans(stmts, n, kind, cols, init, scratch_base) + (True,)
+    return phased_plans(stmts, pairs, n, kind, cols, init, scratch_base) + (True,)
+
+
+def single_pass_plans(stmts, n, init):
     if isinstance(init, DotProdNode):
-        return [dotprod_plan(stmts, init)], 0, False
+        return [dotprod_plan(stmts, init)]
     if isinstance(init, ReduceNode):
-        return [reduce_plan(stmts, init)], 0, False
-    return [elementwise_plan(stmts, n)], 0, False
+        return [reduce_plan(stmts, init)]
+    return [elementwise_plan(stmts, n)]
+
+
+def split_phases(n_stmts, pairs):
+    """Cut the statement list into the fewest consecutive passes such that no
+    conflicting pair lies inside one pass (greedy: a pass ends right before
+    the first statement that conflicts with a statement already in it).
+    Returns ``[(start, end), ...]``."""
+    later = {}
+    for i, j in pairs:
+        later.setdefault(j, []).append(i)
+    phases = []
+    start = 0
+    for j in range(n_stmts):
+        if any(i >= start for i in later.get(j, ())):
+            phases.append((start, j))
+            start = j
+    phases.append((start, n_stmts))
+    return phases
+
+
+def _temp_uses(stmts):
+    """Per statement index: temp ids it reads and the temp id it assigns."""
+    reads, assigns = {}, {}
+    for si, (kind, n) in enumerate(stmts):
+        if kind == "tmp":
+            continue
+        rs = set()
+        for k in n.kargs:
+            for km in _iter_kmatrix(k):
+                if km.is_temp:
+                    rs.add(km.id)
+        reads[si] = rs
+        if not n.kres.is_none() and n.kres.is_temp:
+            assigns[si] = n.kres.id
+    return reads, assigns
+
+
+def phased_plans(stmts, pairs, n, index_kind, n_cols, init_node, scratch_base):
+    """A command whose statements conflict across elements, run as several
+    passes over the elements (one kernel each): the first pass is the
+    DotProd/Reduce (if any) with the statements up to the first conflict in
+    its epilogue, each later pass an elementwise kernel over the same element
+    space.  A temp assigned in one pass and read in a later one is carried
+    through a scratch array indexed by element.  Returns (plans, scratch
+    floats used)."""
+    phases = split_phases(len(stmts), pairs)
+    reads, assigns = _temp_uses(stmts)
+    decl = {node.id: (kind, node) for kind, node in stmts if kind == "tmp"}
+    phase_of_stmt = {}
+    for pi, (a, b) in enumerate(phases):
+        for si in range(a, b):
+            phase_of_stmt[si] = pi
+    assigned_in = {tid: phase_of_stmt[si] for si, tid in assigns.items()}
+    used_in = {}
+    for si, rs in reads.items():
+        for tid in rs:
+            used_in.setdefault(tid, set()).add(phase_of_stmt[si])
+    # scratch slot per temp that crosses a pass boundary
+    slot = {}
+    off = scratch_base
+    stride = (n + 63) // 64 * 64
+    for tid, pa in sorted(assigned_in.items()):
+        if any(pu > pa for pu in used_in.get(tid, ())):
+            slot[tid] = off
+            off += stride
+    plans = []
+    for pi, (a, b) in enumerate(phases):
+        body = [st for st in stmts[a:b] if st[0] != "tmp"]
+        touched = set()
+        for si in range(a, b):
+            touched |= reads.get(si, set())
+            if si in assigns:
+                touched.add(assigns[si])
+        head = []
+        for tid in sorted(touched):
+            if tid in slot and assigned_in[tid] < pi:
+                head.append(("load", (tid, slot[tid])))
+            elif tid in decl:
+                head.append(decl[tid])
+        tail = [("store", (tid, slot[tid])) for tid in sorted(slot) if assigned_in[tid] == pi]
+        part = head + body + tail
+        if pi == 0 and init_node is not None:
+            plans.extend(single_pass_plans(part, n, init_node))
+        else:
+            kind = "global" if init_node is None else ("dp" if isinstance(init_node, DotProdNode) else "red")
+            plans.append(elementwise_plan(part, n, index_kind=kind, n_cols=n_cols))
+    return plans, off - scratch_base

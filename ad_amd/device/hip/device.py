@@ -131,7 +131,7 @@ class HIPDevice(Device):
         sources = {}
         for ps in plans.values():
             for p in ps:
-                sources.setdefault(p.source, None)
+                sources.setdefault(p.source, p.name)
         todo = [s for s in sources if s not in _code_cache]
 
         def build(src):
@@ -142,9 +142,9 @@ class HIPDevice(Device):
                     with _code_lock:
                         _code_cache[src] = code
         funcs = {}
-        for src in sources:
+        for src, name in sources.items():
             mod = self.ctx.load_module(_code_cache[src])
-            funcs[src] = (mod, self.ctx.function(mod, codegen.KNAME))
+            funcs[src] = (mod, self.ctx.function(mod, name))
         self.stats["unique_sources"] += len(sources)
         for pid, ps in plans.items():
             launches = []
@@ -259,6 +259,20 @@ class HIPDevice(Device):
         self._run_proc(proc, self.run, init=False)
         self.ctx.sync()
         self.refresh_tensors()
+
+    # ------------------------------------------------------------------ timing hooks
+    def loops(self, proc):
+        """The ``ForNode`` commands of the top-level Proc, in order."""
+        return [c for c in proc.procedure if isinstance(c, ForNode)]
+
+    def replay(self, loop_cmd, iterations: int):
+        """Run ``iterations`` more iterations of a prepared loop body (a graph
+        replay each when the body is capturable)."""
+        self._run_loop(loop_cmd, iterations)
+
+    def launch(self, cmd):
+        """Enqueue one prepared compute command."""
+        self.funcs[cmd.program_id]()
 
     def refresh_tensors(self):
         """Copy every Tensor buffer back into its host array."""

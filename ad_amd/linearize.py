@@ -12,7 +12,11 @@ change the result:
 * the scan of every fusion attempt starts at the first layer that still holds
   an untaken node able to start a group: earlier layers only hold taken or
   non-starting nodes, which the reference visits without any effect while no
-  group has started yet.
+  group has started yet;
+* the white list of nodes downstream of a blocked node is decided per node
+  as the scan reaches it (``_LazyWhiteList``) instead of walking every later
+  layer at each block (``_EagerWhiteList``, the reference's way, kept as the
+  check); both give the same set at every point of the scan.
 """
 from copy import deepcopy
 from typing import Dict, List
@@ -103,12 +107,64 @@ _FUSION_FAMILIES = [DPElwFuse, ReduceElwFuse, ElwFuse]
 
 
 def _walking_path(start_id, later_layers, deps_of):
+    """fusion/helper.py:70-81: ``start_id`` plus every node of the later
+    layers, scanned in layer order, that depends on a node already in the
+    path."""
     path = set({start_id})
     for layer in later_layers:
         for nid in layer:
             if len(path.intersection(deps_of(nid))) > 0:
                 path.add(nid)
     return path
+
+
+class _EagerWhiteList:
+    """The reference's white list: the union of the walking paths of every
+    start so far, each path computed in full when it starts."""
+
+    def __init__(self, toposort_res, deps_of):
+        self.res, self.deps_of, self.nodes = toposort_res, deps_of, set()
+
+    def reach(self, nid, layer_idx, deps_id):
+        pass
+
+    def start(self, nid, layer_idx):
+        self.nodes.update(_walking_path(nid, self.res[layer_idx + 1:], self.deps_of))
+
+    def __contains__(self, nid):
+        return nid in self.nodes
+
+
+class _LazyWhiteList:
+    """The same set, decided per node when the scan reaches it: node ->
+    lowest start layer among the paths holding it.  A node scanned in layer L
+    is on the path started in layer L0 iff L > L0 and one of its
+    dependencies joined that path earlier in the scan, so scanning in order
+    decides membership without walking any path ahead."""
+
+    def __init__(self, toposort_res, deps_of):
+        self.low = {}
+
+    def reach(self, nid, layer_idx, deps_id):
+        if not self.low:
+            return
+        best = None
+        for d in deps_id:
+            m = self.low.get(d)
+            if m is not None and m < layer_idx and (best is None or m < best):
+                best = m
+        if best is not None:
+            self.low[nid] = best
+
+    def start(self, nid, layer_idx):
+        self.low[nid] = min(self.low.get(nid, layer_idx), layer_idx)
+
+    def __contains__(self, nid):
+        return nid in self.low
+
+
+# the lazy white list is the product path; the eager one is its check
+EAGER_WALKING_PATHS = False
 
 
 def fuse(g_dep_id) -> Proc:
@@ -134,7 +190,7 @@ def fuse(g_dep_id) -> Proc:
         first_layer = 0
         while True:
             op_entry = family()
-            white_list_nodes = set()
+            white = (_EagerWhiteList if EAGER_WALKING_PATHS else _LazyWhiteList)(toposort_res, deps_of)
             did_start = False
             # skip leading layers in which no untaken node can start a group
             while first_layer < len(toposort_res) and not any(
@@ -146,12 +202,12 @@ def fuse(g_dep_id) -> Proc:
                 did_sum = False
                 for nid in layer:
                     deps_id = deps_of(nid)
+                    white.reach(nid, layer_idx, deps_id)
                     if nid in init_taken:
                         if len(deps_id.intersection(op_entry.result_tracker)) > 0:
-                            white_list_nodes.update(
-                                _walking_path(nid, toposort_res[layer_idx + 1:], deps_of))
+                            white.start(nid, layer_idx)
                         continue
-                    if nid in white_list_nodes:
+                    if nid in white:
                         continue
                     result = op_entry.attempt_fuse(id_to_node[nid], deps_id)
                     if result in (FuseResult.ADD, FuseResult.INIT):
@@ -159,8 +215,7 @@ def fuse(g_dep_id) -> Proc:
                         did_sum = True
                         did_start = True
                     elif len(deps_id.intersection(op_entry.result_tracker)) > 0:
-                        white_list_nodes.update(
-                            _walking_path(nid, toposort_res[layer_idx + 1:], deps_of))
+                        white.start(nid, layer_idx)
                 if did_start and not did_sum:
                     break
             if len(op_entry.nodes) == 0:

@@ -30,13 +30,15 @@ def _intern_repeat_opt(context) -> int:
     context.procedure[0] = walk_graph(context.procedure[0], track_nodes)
     dupes = [nodes for nodes in groups.values() if len(nodes) > 1]
 
+    # the first group whose later members include the node's id decides
+    # (the reference scans the groups in order for every node)
+    keep_of = {}
+    for nodes in dupes:
+        for v in nodes[1:]:
+            keep_of.setdefault(v.id, nodes[0])
+
     def replace_node(node, _):
-        for nodes in dupes:
-            keep = nodes[0]
-            drop = set([v.id for v in nodes[1:]])
-            if node.id in drop:
-                return keep
-        return node
+        return keep_of.get(node.id, node)
 
     context.procedure[0] = walk_graph(context.procedure[0], replace_node)
     return len(dupes)

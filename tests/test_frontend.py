@@ -272,3 +272,94 @@ def test_permute_non_involution_follows_reference():
     got = [evaluate(cmd.kargs[0].access, g=g) for g in range(27)]
     assert got == np.transpose(idx, inv).reshape(-1).tolist()
     assert got != np.transpose(idx, perm).reshape(-1).tolist()
+
+
+# ---------------------------------------------------------------- fast passes
+# The compile passes below are rewritten for speed (the reference's versions
+# are quadratic in the graph size); each check compares the product version
+# with a direct restatement of the reference's loop.
+
+def _toposort_direct(data):
+    """The ``toposort`` package's loop: emit the keys with no remaining
+    dependencies, subtract them from every other set, repeat."""
+    from functools import reduce
+    data = data.copy()
+    for item, deps in data.items():
+        deps.discard(item)
+    extra = reduce(set.union, data.values()) - set(data.keys())
+    data.update({item: set() for item in extra})
+    while True:
+        ordered = set(item for item, dep in data.items() if len(dep) == 0)
+        if not ordered:
+            break
+        yield ordered
+        data = {item: (dep - ordered) for item, dep in data.items() if item not in ordered}
+    if len(data) != 0:
+        raise ValueError("cycle")
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_toposort_matches_direct_loop(seed):
+    """Same layers and the same iteration order inside every layer (the
+    order decides command order and so arena offsets)."""
+    import random
+    from ad_amd.toposort import toposort
+    rng = random.Random(seed)
+    n = rng.randint(1, 300)
+    ids = rng.sample(range(10000), n)
+    data = {}
+    for i, x in enumerate(ids):
+        deps = set(rng.sample(ids[:i], min(rng.randint(0, 4), i)))
+        if rng.random() < 0.1:
+            deps.add(x)                              # self edges are dropped
+        deps |= set(rng.sample(range(10000, 10100), rng.randint(0, 2)))   # keys added
+        data[x] = deps
+    want = [list(s) for s in _toposort_direct({k: set(v) for k, v in data.items()})]
+    got = [list(s) for s in toposort({k: set(v) for k, v in data.items()})]
+    assert got == want
+
+
+def test_toposort_reports_cycles():
+    from ad_amd.toposort import CircularDependencyError, toposort
+    with pytest.raises(CircularDependencyError):
+        list(toposort({1: {2}, 2: {3}, 3: {1}, 4: set()}))
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_tetris_place_matches_direct_loop(seed):
+    import copy
+    import random
+    from ad_amd.alloc.tetris_opt import VarEntry, place, place_reference
+    rng = random.Random(seed)
+    entries = []
+    for v in range(rng.randint(0, 150)):
+        s0 = rng.randint(0, 100)
+        entries.append(VarEntry(v, s0, s0 + rng.randint(0, 30), rng.choice([0, 1, 2, 4, 8, rng.randint(1, 64)])))
+    entries.sort(key=lambda e: -e.size)
+    a, b = copy.deepcopy(entries), copy.deepcopy(entries)
+    assert place(a) == place_reference(b)
+    assert [e.offset for e in a] == [e.offset for e in b]
+
+
+@pytest.mark.parametrize("build", ["mlp", "layernorm", "transformer", "batched"])
+def test_lazy_white_list_matches_walking_paths(build):
+    """The whole compiled Proc (command order, fused groups, access
+    expressions, arena offsets) is identical with the reference's eager
+    walking paths and with the lazy white list."""
+    from ad_amd import linearize, workloads
+    builders = {
+        "mlp": lambda: workloads.mlp(steps=2, din=16, dh=24, dout=8),
+        "layernorm": lambda: workloads.layernorm_train(rows=8, cols=16, steps=2),
+        "transformer": lambda: workloads.transformer(layers=1, d_model=32, heads=4, ff=64, seq=4, steps=2),
+        "batched": lambda: workloads.transformer(layers=2, d_model=32, heads=4, ff=64, seq=8, batch=3, steps=1),
+    }
+    out = []
+    for eager in (False, True):
+        ad.reset()
+        linearize.EAGER_WALKING_PATHS = eager
+        try:
+            builders[build]()
+            out.append(repr(ad.compile_proc()))
+        finally:
+            linearize.EAGER_WALKING_PATHS = False
+    assert out[0] == out[1]

@@ -134,3 +134,21 @@ def test_layernorm_training_parity(hip):
 def test_transformer_parity(hip):
     a, b = run_both(lambda: programs.transformer(layers=1, d_model=32, heads=4, ff=64, seq=4, steps=2), hip)
     assert_params_close(a, b)
+
+
+def test_batched_transformer_parity(hip):
+    """Two sequences per batch (per-sample attention on Index slices, rows
+    concatenated back): exercises commands split into several passes where
+    the arena reuses a slot inside a fused group."""
+    from ad_amd import workloads
+    a, b = run_both(lambda: workloads.transformer(layers=2, d_model=32, heads=4, ff=64, seq=8, batch=2,
+                                                  steps=2), hip)
+    assert_params_close(a, b)
+
+
+def test_layernorm_wide_parity(hip):
+    """LayerNorm fwd+bwd at 64 x 1024 (row reductions of 1024 and column
+    reductions of 64) for 2 SGD steps on gamma/beta."""
+    from ad_amd import workloads
+    a, b = run_both(lambda: workloads.layernorm_train(rows=64, cols=1024, steps=2), hip)
+    assert_params_close(a, b)
