@@ -62,12 +62,41 @@ class KernelPlan:
         # every template emits the symbol KNAME; give each distinct source its
         # own symbol so profiles tell kernels apart
         tag = {"dotprod": "dp", "reduce": "red", "elw": "elw", "copy": "copy"}.get(self.family, "k")
+        self.source = _table_entry(self.source, len(self.args))
         self.name = f"adhip_{tag}_{hashlib.sha1(self.source.encode()).hexdigest()[:12]}"
         self.source = self.source.replace(KNAME, self.name)
 
     @property
     def key(self):
         return self.name
+
+
+_ENTRY_RE = re.compile(r'extern "C" __global__ void __launch_bounds__\((\d+)\) ' + "adhip_kernel" + r"\(([^)]*)\) \{")
+
+
+def _table_entry(src: str, nargs: int) -> str:
+    """Turn the generated kernel (the last function of ``src``) into a device
+    function plus an entry point whose only parameter is an argument table
+    in device memory: row ``blockIdx.z`` holds the 8-byte arguments (pointers
+    and integers) of one instance, so one launch can run several independent
+    commands that share the kernel."""
+    m = _ENTRY_RE.search(src)
+    assert m is not None, "generated kernel entry not found"
+    bounds, params = m.group(1), m.group(2)
+    plist = [q.strip() for q in params.split(",") if q.strip()]
+    assert len(plist) == nargs, (plist, nargs)
+    end = src.rindex("}")
+    body = src[m.end():end]
+    casts = []
+    for i, q in enumerate(plist):
+        ty = q.rsplit(" ", 1)[0]
+        casts.append(f"({ty})a_[{i}]")
+    return (src[:m.start()] +
+            f"static __device__ __forceinline__ void {KNAME}_body({params}) {{{body}}}\n"
+            f'extern "C" __global__ void __launch_bounds__({bounds}) {KNAME}('
+            f"const unsigned long long* __restrict__ tbl_) {{\n"
+            f"  const unsigned long long* a_ = tbl_ + (unsigned long long)blockIdx.z * {max(nargs, 1)}u;\n"
+            f"  (void)a_;\n  {KNAME}_body({', '.join(casts)});\n}}\n")
 
 
 # ------------------------------------------------------------------ statements
@@ -182,25 +211,54 @@ def conflict_pairs(stmts, buffers: BufferInfo, index_kind: str, n_cols: int = 1)
     return sorted(out)
 
 
+def command_regions(cmd, buffers: BufferInfo):
+    """Buffer ranges ``(buffer, lo, hi)`` (floats) a command may read and may
+    write: the packed region of each arena variable it addresses, or the
+    whole buffer otherwise."""
+    nodes = cmd.nodes if hasattr(cmd, "nodes") else [cmd]
+    reads, writes = set(), set()
+    for kind, n in statements(nodes):
+        if kind == "tmp":
+            continue
+        for k in n.kargs:
+            for km in _iter_kmatrix(k):
+                if not km.is_temp:
+                    reads.add(_region(km, buffers)[0])
+        if not n.kres.is_none() and not n.kres.is_temp:
+            writes.add(_region(n.kres, buffers)[0])
+    return sorted(reads, key=repr), sorted(writes, key=repr)
+
+
 def hazards(stmts, buffers: BufferInfo, index_kind: str, n_cols: int = 1) -> bool:
     """True when the command needs more than one pass over its elements."""
     return len(conflict_pairs(stmts, buffers, index_kind, n_cols)) > 0
 
 
 # ------------------------------------------------------------------ lowering helpers
+MAX_PTR_PARAMS = 48
+
+
 class Params:
-    """Kernel pointer parameters keyed by (buffer id, folded offset)."""
+    """Kernel pointer parameters keyed by (buffer id, folded offset).  Past
+    ``MAX_PTR_PARAMS`` distinct pointers, further offsets are added to the
+    buffer's base pointer in the source instead (a command that touches
+    hundreds of arena slots compiles to its own kernel either way)."""
 
     def __init__(self):
         self.slots: List[tuple] = []
         self.index: Dict[tuple, int] = {}
 
-    def ptr(self, kind, ident, offset) -> str:
-        key = (kind, ident, offset)
+    def _slot(self, key) -> int:
         if key not in self.index:
             self.index[key] = len(self.slots)
             self.slots.append(key)
-        return f"p{self.index[key]}"
+        return self.index[key]
+
+    def ptr(self, kind, ident, offset) -> str:
+        key = (kind, ident, offset)
+        if key in self.index or len(self.slots) < MAX_PTR_PARAMS or offset == 0:
+            return f"p{self._slot(key)}"
+        return f"(p{self._slot((kind, ident, 0))} + {offset}LL)"
 
 
 def lower_index(e, ity) -> str:

@@ -6,8 +6,14 @@ replays loop bodies, ``execute`` runs both passes.  Differences by design:
 
 * every buffer lives in ONE device allocation (the arena) at a 256-byte
   aligned offset; the tetris region keeps the allocator's float offsets;
+  after the buffers come the Feeder staging slots, the scratch region of
+  multi-pass commands and the kernel argument tables;
 * kernels are generated per command (``codegen``), deduplicated by source
   text and compiled in parallel through hipRTC at the end of the init pass;
+  every kernel reads its arguments from a row of an argument table;
+* each stretch of commands between Feeders/Receivers/loops is scheduled
+  (``schedule``): launches ordered by their memory conflicts, and
+  independent launches of one kernel merged into one launch;
 * a loop body without Receivers is captured once as a HIP graph and the
   graph is replayed ``len(r)`` times; a Feeder inside it copies from its own
   staging slot, refilled from the host before each replay;
@@ -30,6 +36,7 @@ from ...node import Node
 from .. import Device
 from . import codegen
 from .runtime import HEADER_PATH, Context, compile_source
+from .schedule import schedule
 
 ALIGN = 256
 _code_cache = {}            # source text -> code object (process-wide)
@@ -45,22 +52,35 @@ def _header():
         return fh.read()
 
 
+class _Launch:
+    """One kernel launch: a plan of a command, its argument row, the
+    ranges it reads and writes."""
+    __slots__ = ("cmd", "plan", "args", "reads", "writes")
+
+    def __init__(self, cmd, plan, args, reads, writes):
+        self.cmd, self.plan, self.args, self.reads, self.writes = cmd, plan, args, reads, writes
+
+
 class HIPDevice(Device):
-    def __init__(self, device_index: int = 0, use_graphs: bool = True, jit_threads: int = None):
+    def __init__(self, device_index: int = 0, use_graphs: bool = True, jit_threads: int = None,
+                 group_launches: bool = True):
         super().__init__()
         self.kernels = {}            # program_id -> [KernelPlan]
-        self.funcs = {}              # program_id -> launch callable
+        self.funcs = {}              # program_id -> launch callable (ungrouped)
         self.buffers = {}            # buffer id -> arena byte offset
         self.buffers_size = {}       # buffer id -> floats
         self.use_graphs = use_graphs
+        self.group_launches = group_launches
         self.jit_threads = jit_threads or min(16, (os.cpu_count() or 4))
         self.ctx = Context(device_index)
         self._allocs = []
         self._contents = {}
         self._pending = []
         self._feeder_slots = {}      # feeder id -> staging byte offset
-        self._graphs = {}            # ForNode id -> graph handle
-        self.stats = {"kernels": 0, "unique_sources": 0, "lockstep_cmds": 0, "launches_per_iter": 0}
+        self._graphs = {}            # ForNode id -> (graph handle, feeders)
+        self._schedules = {}         # Proc id -> [("launch", fn) | ("cmd", cmd)]
+        self._capturing = False
+        self.stats = {"kernels": 0, "unique_sources": 0, "multipass_cmds": 0, "launches_per_iter": 0}
 
     # ------------------------------------------------------------------ init pass
     def init(self, cmd):
@@ -88,8 +108,7 @@ class HIPDevice(Device):
         raise AssertionError(f"Encountered unexpected cmd: {cmd}")
 
     def _layout(self):
-        """Arena: every non-temp AllocEntry, then Feeder staging slots, then
-        scratch for lockstep commands."""
+        """Byte offset of every non-temp buffer, in AllocEntry order."""
         off = 0
         info = codegen.BufferInfo()
         for a in self._allocs:
@@ -101,38 +120,140 @@ class HIPDevice(Device):
             off += _align(a.size * 4)
         return off, info
 
-    def _finish_init(self):
+    def _finish_init(self, proc):
         off, info = self._layout()
-        # Feeder staging slots (used when a Feeder runs inside a captured graph)
         for fid in list(self._feeder_slots):
             self._feeder_slots[fid] = off
-            size = self._feeder_size.get(fid, 0)
-            off += _align(size * 4)
-        scratch_base = off
-        # generate plans
+            off += _align(self._feeder_size.get(fid, 0) * 4)
+        # kernel plans and the ranges each command touches
         scratch_need = 0
-        plans = {}
+        plans, regions = {}, {}
         for cmd in self._pending:
-            ps, need, lockstep = codegen.command_plans(cmd, info, 0)
+            ps, need, multipass = codegen.command_plans(cmd, info, 0)
             plans[cmd.program_id] = ps
+            reads, writes = codegen.command_regions(cmd, info)
+            if need:
+                reads.append(("scratch", 0, need))
+                writes.append(("scratch", 0, need))
+            regions[cmd.program_id] = (reads, writes)
             scratch_need = max(scratch_need, need)
-            self.stats["lockstep_cmds"] += int(lockstep)
+            self.stats["multipass_cmds"] += int(multipass)
+        self.scratch_off = off
         off += _align(scratch_need * 4)
+        # schedule every stretch of every Proc, then lay out argument tables
+        rows = []                      # (byte offset in table region, [u64 values])
+        table_bytes = [0]
+
+        def add_rows(values_list):
+            start = table_bytes[0]
+            for vals in values_list:
+                rows.append((table_bytes[0], vals))
+                table_bytes[0] += 8 * max(1, len(vals))
+            return start
+
+        self._plans = plans
+        launch_rows = {}               # program_id -> [row offsets per plan]
+        for pid, ps in plans.items():
+            launch_rows[pid] = [add_rows([self._arg_values(p)]) for p in ps]
+        sched = self._build_schedules(proc, plans, regions, add_rows)
+        self.table_off = off
+        off += _align(max(table_bytes[0], 8))
         self.ctx.reserve(max(off, ALIGN))
-        self.scratch_off = scratch_base
         for bid, content in self._contents.items():
             assert content.dtype == np.float32, "Content is not np.float32"
             self.ctx.write(self.buffers[bid], np.ascontiguousarray(content))
-        self._compile_and_bind(plans)
+        table = np.zeros(max(table_bytes[0], 8) // 8, dtype=np.uint64)
+        base = self.ctx.base
+        for boff, vals in rows:
+            for i, (is_ptr, v) in enumerate(vals):
+                table[boff // 8 + i] = (base + v) if is_ptr else v
+        self.ctx.write(self.table_off, table)
+        funcs = self._compile(plans)
+        self.stats["unique_sources"] += len(funcs)
+        tbase = self.ctx.base + self.table_off
+        for pid, ps in plans.items():
+            launches = [self.ctx.launcher(funcs[p.name], p.grid, p.block, p.shared, [tbase + r])
+                        for p, r in zip(ps, launch_rows[pid])]
+            self.kernels[pid] = ps
+            self.stats["kernels"] += len(ps)
+            self.funcs[pid] = launches[0] if len(launches) == 1 else (lambda ls=launches: [f() for f in ls])
+        for pid_proc, items in sched.items():
+            out = []
+            for item in items:
+                if item[0] == "cmd":
+                    out.append(item)
+                    continue
+                _, plan, row, count = item
+                grid = (plan.grid[0], plan.grid[1], count)
+                out.append(("launch", self.ctx.launcher(funcs[plan.name], grid, plan.block, plan.shared,
+                                                        [tbase + row])))
+            self._schedules[pid_proc] = out
         self._pending = []
 
-    def _compile_and_bind(self, plans):
+    def _arg_values(self, plan):
+        """Argument row of a plan: ``(True, arena byte offset)`` for a pointer
+        (resolved against the arena base once it exists), ``(False, v)`` for
+        an integer."""
+        vals = []
+        for a in plan.args:
+            if a[0] == "buf":
+                vals.append((True, self.buffers[a[1]] + 4 * a[2]))
+            elif a[0] == "scratch":
+                vals.append((True, self.scratch_off + 4 * a[1]))
+            else:
+                vals.append((False, int(a[1]) & 0xFFFFFFFFFFFFFFFF))
+        return vals
+
+    def _build_schedules(self, proc, plans, regions, add_rows):
+        """Per Proc: the launch order and grouping of each stretch of kernel
+        commands between Feeders, Receivers and loops."""
+        out = {}
+
+        def visit(p):
+            items = []
+            stretch = []
+
+            def flush():
+                if not stretch:
+                    return
+                launches = []
+                for cmd in stretch:
+                    reads, writes = regions[cmd.program_id]
+                    for plan in plans[cmd.program_id]:
+                        launches.append(_Launch(cmd, plan, None, reads, writes))
+                key = (lambda L: (L.plan.name, L.plan.grid, L.plan.block, L.plan.shared)) \
+                    if self.group_launches else (lambda L: None)
+                for group in schedule([(L, L.reads, L.writes) for L in launches], key):
+                    members = [launches[i] for i in group]
+                    plan = members[0].plan
+                    row = add_rows([self._arg_values(m.plan) for m in members])
+                    items.append(("launch", plan, row, len(members)))
+                stretch.clear()
+
+            for cmd in p.procedure:
+                if isinstance(cmd, (AllocEntry, DeallocEntry)):
+                    continue
+                if isinstance(cmd, (Feeder, Receiver, ForNode)):
+                    flush()
+                    items.append(("cmd", cmd))
+                    if isinstance(cmd, ForNode):
+                        visit(cmd.get_proc())
+                    continue
+                stretch.append(cmd)
+            flush()
+            out[p.id] = items
+
+        visit(proc)
+        return out
+
+    def _compile(self, plans):
+        """hipRTC-compile every distinct kernel (in parallel) and load it."""
         header = _header()
         sources = {}
         for ps in plans.values():
             for p in ps:
-                sources.setdefault(p.source, p.name)
-        todo = [s for s in sources if s not in _code_cache]
+                sources.setdefault(p.name, p.source)
+        todo = [src for src in sources.values() if src not in _code_cache]
 
         def build(src):
             return src, compile_source(header + src)
@@ -142,28 +263,10 @@ class HIPDevice(Device):
                     with _code_lock:
                         _code_cache[src] = code
         funcs = {}
-        for src, name in sources.items():
+        for name, src in sources.items():
             mod = self.ctx.load_module(_code_cache[src])
-            funcs[src] = (mod, self.ctx.function(mod, name))
-        self.stats["unique_sources"] += len(sources)
-        for pid, ps in plans.items():
-            launches = []
-            for p in ps:
-                args = []
-                for a in p.args:
-                    if a[0] == "buf":
-                        args.append(self.ctx.base + self.buffers[a[1]] + 4 * a[2])
-                    elif a[0] == "scratch":
-                        args.append(self.ctx.base + self.scratch_off + 4 * a[1])
-                    else:
-                        args.append(a[1])
-                launches.append(self.ctx.launcher(funcs[p.source][1], p.grid, p.block, p.shared, args))
-            self.kernels[pid] = ps
-            self.stats["kernels"] += len(ps)
-            if len(launches) == 1:
-                self.funcs[pid] = launches[0]
-            else:
-                self.funcs[pid] = (lambda ls=launches: [f() for f in ls])
+            funcs[name] = self.ctx.function(mod, name)
+        return funcs
 
     # ------------------------------------------------------------------ run pass
     def run(self, cmd):
@@ -198,37 +301,44 @@ class HIPDevice(Device):
     def _capturable(self, proc):
         return not any(isinstance(c, (Receiver, ForNode)) for c in proc.procedure)
 
+    def _run_scheduled(self, proc):
+        for item in self._schedules[proc.id]:
+            if item[0] == "launch":
+                item[1]()
+            elif isinstance(item[1], ForNode):
+                self._run_loop(item[1])
+            else:
+                self.run(item[1])
+
     def _run_loop(self, cmd, iterations=None):
         inner = cmd.get_proc()
+        assert inner is not None, "Inner proc is None!"
         reps = len(cmd.r) if iterations is None else iterations
         if reps <= 0:
             return
         if not (self.use_graphs and self._capturable(inner)):
             for _ in range(reps):
-                self._run_proc(inner, self.run, False)
+                self._run_scheduled(inner)
             return
-        g = self._graphs.get(cmd.id)
-        if g is None:
+        if cmd.id not in self._graphs:
             self._capturing = True
             self._graph_feeders = []
             self.ctx.graph_begin()
             try:
-                self._run_proc(inner, self.run, False)
+                self._run_scheduled(inner)
             finally:
                 self._capturing = False
                 g = self.ctx.graph_end()
             self._graphs[cmd.id] = (g, self._graph_feeders)
-        else:
-            g, feeders = g
-            self._graph_feeders = feeders
-        g = self._graphs[cmd.id][0]
-        feeders = self._graphs[cmd.id][1]
+        g, feeders = self._graphs[cmd.id]
         for _ in range(reps):
             for f in feeders:
                 self.ctx.write(self._feeder_slots[f.id], self._feeder_value(f))
             self.ctx.graph_launch(g)
 
     def _run_proc(self, proc, func, init=False):
+        """The reference's command walk (device.py:114-124), used for the init
+        pass; the run pass goes through the schedules."""
         for cmd in proc.procedure:
             if isinstance(cmd, ForNode):
                 inner = cmd.get_proc()
@@ -242,7 +352,7 @@ class HIPDevice(Device):
 
     # ------------------------------------------------------------------ driver
     def prepare(self, proc):
-        """Init pass: layout, upload, JIT."""
+        """Init pass: layout, upload, JIT, schedules."""
         self._capturing = False
         self._feeder_size = {}
 
@@ -252,11 +362,14 @@ class HIPDevice(Device):
             return c
         proc.walk(note_feeders, step_fused=False, step_proc=True)
         self._run_proc(proc, self.init, init=True)
-        self._finish_init()
+        self._finish_init(proc)
+        for loop in self.loops(proc):
+            self.stats["launches_per_iter"] = sum(1 for it in self._schedules[loop.get_proc().id]
+                                                  if it[0] == "launch")
 
     def execute(self, proc):
         self.prepare(proc)
-        self._run_proc(proc, self.run, init=False)
+        self._run_scheduled(proc)
         self.ctx.sync()
         self.refresh_tensors()
 
@@ -271,7 +384,7 @@ class HIPDevice(Device):
         self._run_loop(loop_cmd, iterations)
 
     def launch(self, cmd):
-        """Enqueue one prepared compute command."""
+        """Enqueue one prepared compute command (its own launches, ungrouped)."""
         self.funcs[cmd.program_id]()
 
     def refresh_tensors(self):

@@ -130,7 +130,7 @@ def micro_elw(reps, copies=2):
     return {"kernel": name, "ms": ms, "bytes": nbytes, "gbs": nbytes / ms / 1e6}
 
 
-def transformer_steps(config, steps, warmup):
+def transformer_steps(config, steps, warmup, eager=False):
     import ad_amd as ad
     from ad_amd import workloads
     from ad_amd.device.hip import HIPDevice
@@ -143,7 +143,7 @@ def transformer_steps(config, steps, warmup):
     t1 = time.perf_counter()
     step_flops = workloads.dotprod_flops(proc)
     log(f"{config}: traced + compiled in {t1 - t0:.1f} s; {step_flops / 1e12:.3f} TFLOP of DotProd per step")
-    dev = HIPDevice()
+    dev = HIPDevice(use_graphs=not eager)
     dev.prepare(proc)
     t2 = time.perf_counter()
     log(f"{config}: device init + JIT in {t2 - t1:.1f} s; {dev.stats}")
@@ -160,8 +160,7 @@ def transformer_steps(config, steps, warmup):
     dev.ctx.sync()
     t4 = time.perf_counter()
     ev_ms = dev.ctx.elapsed_ms(0, 1)
-    inner = loop.get_proc()
-    launches = sum(len(dev.kernels[c.program_id]) for c in _commands(inner))
+    launches = dev.stats["launches_per_iter"]
     dev.close()
     return {"wall_s": t4 - t3, "event_ms": ev_ms, "step_flops": step_flops,
             "compile_s": t1 - t0, "init_s": t2 - t1, "launches_per_step": launches}
@@ -220,6 +219,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-micro", action="store_true", help="skip the single-command benchmarks")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch the step's kernels one by one instead of replaying a HIP graph "
+                         "(for kernel-trace profilers)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -246,7 +248,7 @@ def main():
                          "gbs": round(elw["gbs"], 1), "frac": round(elw["gbs"] / PEAK_HBM_GBS, 4)},
         }
 
-    tr = transformer_steps(args.config, args.steps, args.warmup)
+    tr = transformer_steps(args.config, args.steps, args.warmup, eager=args.eager)
     value = args.steps / tr["wall_s"]
     ms_per_step = tr["wall_s"] * 1e3 / args.steps
     log(f"{args.config}: {ms_per_step:.2f} ms/step wall, {tr['event_ms'] / args.steps:.2f} ms/step "
@@ -274,7 +276,7 @@ def main():
         "data": "synthetic",
         "config": {"workload": f"{args.config}: {layers}-layer transformer encoder fwd+bwd+SGD, "
                                f"d_model {d}, {h} heads, FFN {f} ReLU, seq {s}, batch {b}, fp32, "
-                               "one HIP-graph replay per step",
+                               + ("eager launches" if args.eager else "one HIP-graph replay per step"),
                    "layers": layers, "d_model": d, "heads": h, "ffn": f, "seq_len": s, "batch": b,
                    "parallelism": "none (1 GPU)"},
         "step_dotprod_tflops": round(tr["step_flops"] / (ms_per_step * 1e9), 2),
