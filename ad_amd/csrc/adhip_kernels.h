@@ -3,13 +3,15 @@
 // loaders with the access expression inlined, and an epilogue with the fused
 // elementwise statements) and instantiates one of the templates below.
 //
-//  * dp_mfma      -- DotProd+Elw: fp32 MFMA (v_mfma_f32_32x32x2_f32), 128x128
-//                    block tile, 4 waves of 64x64, LDS-staged K panels with a
-//                    register prefetch of the next panel, epilogue in registers.
+//  * dp_mfma      -- DotProd+Elw: fp32 MFMA (v_mfma_f32_32x32x2_f32), BM x BN
+//                    block tile (64..256), 4 waves, LDS-staged K panels with a
+//                    register prefetch of the next panel, optional split of K
+//                    into chunks, epilogue in registers.
 //  * reduce_rows  -- Reduce+Elw, rows contiguous: one wave per row, float4 or
 //                    scalar coalesced loads, butterfly over the wave.
 //  * reduce_cols  -- Reduce+Elw, columns contiguous: 64 columns x 4 row groups
-//                    per block, coalesced along the columns, LDS combine.
+//                    per block, coalesced along the columns, LDS combine,
+//                    optional split of the rows into chunks.
 // Elementwise (ElwFuse) kernels are emitted whole by the generator.
 #pragma clang fp contract(off)
 
@@ -28,184 +30,208 @@ __device__ __forceinline__ float rop(float a, float b) {
 // LA::at4 / LB::at4 load 4 consecutive elements along the contiguous axis.
 // LA::kMode: 0 = contiguous along k, 1 = contiguous along m.
 // LB::kMode: 0 = contiguous along n, 1 = contiguous along k.
-constexpr int DP_BM = 128, DP_BN = 128, DP_BK = 16, DP_PAD = 4;
+//
+// Block tile BM x BN, K panels of DP_BK staged in LDS, 4 waves as 2 x 2, each
+// wave (BM/2) x (BN/2) made of 32x32 v_mfma_f32_32x32x2f32 tiles; the next
+// panel is prefetched into registers while the current one is consumed.
+// SPLIT > 1 splits K into SPLIT chunks: blockIdx.y = tile row + tiles_m *
+// chunk, and the epilogue receives the chunk index (partial results).
+// The epilogue is called as epi(value, row, col, chunk) in registers.
+constexpr int DP_BK = 16, DP_PAD = 4;
 
-template <class LA, class LB, class EPI>
+template <int BM, int BN, int SPLIT, class LA, class LB, class EPI>
 __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& epi, int M, int N, int K) {
-  __shared__ float As[DP_BK][DP_BM + DP_PAD];
-  __shared__ float Bs[DP_BK][DP_BN + DP_PAD];
+  static_assert(BM % 64 == 0 && BN % 64 == 0, "tile must be a multiple of 64");
+  constexpr int TM = BM / 64, TN = BN / 64;              // 32x32 tiles per wave
+  constexpr int VA = BM * DP_BK / 4 / 256;               // float4 loads per thread
+  constexpr int VB = BN * DP_BK / 4 / 256;
+  static_assert(VA >= 1 && VB >= 1, "tile too small for 256 threads");
+  __shared__ float As[DP_BK][BM + DP_PAD];
+  __shared__ float Bs[DP_BK][BN + DP_PAD];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int m0 = blockIdx.y * DP_BM, n0 = blockIdx.x * DP_BN;
+  const int tiles_m = (M + BM - 1) / BM;
+  const int by = blockIdx.y;
+  const int chunk = SPLIT > 1 ? by / tiles_m : 0;
+  const int m0 = (SPLIT > 1 ? by % tiles_m : by) * BM, n0 = blockIdx.x * BN;
+  int kbeg = 0, kend = K;
+  if constexpr (SPLIT > 1) {
+    const int kc = ((K + SPLIT - 1) / SPLIT + DP_BK - 1) / DP_BK * DP_BK;
+    kbeg = chunk * kc;
+    kend = kbeg + kc < K ? kbeg + kc : K;
+  }
 
-  float ra[8], rb[8];
+  float ra[VA][4], rb[VB][4];
 
   auto load_a = [&](int k0) {
-    if constexpr (LA::kMode == 0) {            // thread: one row, 8 consecutive k
-      const int m = m0 + (tid >> 1);
-      const int kb = k0 + (tid & 1) * 8;
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int k = kb + 4 * h;
+    for (int i = 0; i < VA; ++i) {
+      const int v = tid + 256 * i;
+      if constexpr (LA::kMode == 0) {          // row of 4 consecutive k
+        const int m = m0 + v / (DP_BK / 4), k = k0 + 4 * (v % (DP_BK / 4));
         if constexpr (LA::kVec) {
-          float4 v = (m < M && k < K) ? la.at4(m, k) : make_float4(0.f, 0.f, 0.f, 0.f);
-          ra[4 * h + 0] = v.x; ra[4 * h + 1] = v.y; ra[4 * h + 2] = v.z; ra[4 * h + 3] = v.w;
+          const float4 x = (m < M && k < kend) ? la.at4(m, k) : make_float4(0.f, 0.f, 0.f, 0.f);
+          ra[i][0] = x.x; ra[i][1] = x.y; ra[i][2] = x.z; ra[i][3] = x.w;
         } else {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) ra[4 * h + j] = (m < M && k + j < K) ? la.at(m, k + j) : 0.f;
+          for (int j = 0; j < 4; ++j) ra[i][j] = (m < M && k + j < kend) ? la.at(m, k + j) : 0.f;
         }
-      }
-    } else {                                    // thread: one k, 8 consecutive rows
-      const int k = k0 + (tid >> 4);
-      const int mb = m0 + (tid & 15) * 8;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int m = mb + 4 * h;
+      } else {                                  // k row of 4 consecutive m
+        const int k = k0 + v / (BM / 4), m = m0 + 4 * (v % (BM / 4));
         if constexpr (LA::kVec) {
-          float4 v = (k < K && m < M) ? la.at4(m, k) : make_float4(0.f, 0.f, 0.f, 0.f);
-          ra[4 * h + 0] = v.x; ra[4 * h + 1] = v.y; ra[4 * h + 2] = v.z; ra[4 * h + 3] = v.w;
+          const float4 x = (k < kend && m < M) ? la.at4(m, k) : make_float4(0.f, 0.f, 0.f, 0.f);
+          ra[i][0] = x.x; ra[i][1] = x.y; ra[i][2] = x.z; ra[i][3] = x.w;
         } else {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) ra[4 * h + j] = (k < K && m + j < M) ? la.at(m + j, k) : 0.f;
+          for (int j = 0; j < 4; ++j) ra[i][j] = (k < kend && m + j < M) ? la.at(m + j, k) : 0.f;
         }
       }
     }
   };
   auto store_a = [&]() {
-    if constexpr (LA::kMode == 0) {
-      const int m = tid >> 1, kb = (tid & 1) * 8;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) As[kb + j][m] = ra[j];
-    } else {
-      const int k = tid >> 4, mb = (tid & 15) * 8;
-      *reinterpret_cast<float4*>(&As[k][mb]) = make_float4(ra[0], ra[1], ra[2], ra[3]);
-      *reinterpret_cast<float4*>(&As[k][mb + 4]) = make_float4(ra[4], ra[5], ra[6], ra[7]);
+    for (int i = 0; i < VA; ++i) {
+      const int v = tid + 256 * i;
+      if constexpr (LA::kMode == 0) {
+        const int m = v / (DP_BK / 4), k = 4 * (v % (DP_BK / 4));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) As[k + j][m] = ra[i][j];
+      } else {
+        const int k = v / (BM / 4), m = 4 * (v % (BM / 4));
+        *reinterpret_cast<float4*>(&As[k][m]) = make_float4(ra[i][0], ra[i][1], ra[i][2], ra[i][3]);
+      }
     }
   };
   auto load_b = [&](int k0) {
-    if constexpr (LB::kMode == 0) {            // thread: one k, 8 consecutive n
-      const int k = k0 + (tid >> 4);
-      const int nb = n0 + (tid & 15) * 8;
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int n = nb + 4 * h;
+    for (int i = 0; i < VB; ++i) {
+      const int v = tid + 256 * i;
+      if constexpr (LB::kMode == 0) {          // k row of 4 consecutive n
+        const int k = k0 + v / (BN / 4), n = n0 + 4 * (v % (BN / 4));
         if constexpr (LB::kVec) {
-          float4 v = (k < K && n < N) ? lb.at4(k, n) : make_float4(0.f, 0.f, 0.f, 0.f);
-          rb[4 * h + 0] = v.x; rb[4 * h + 1] = v.y; rb[4 * h + 2] = v.z; rb[4 * h + 3] = v.w;
+          const float4 x = (k < kend && n < N) ? lb.at4(k, n) : make_float4(0.f, 0.f, 0.f, 0.f);
+          rb[i][0] = x.x; rb[i][1] = x.y; rb[i][2] = x.z; rb[i][3] = x.w;
         } else {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) rb[4 * h + j] = (k < K && n + j < N) ? lb.at(k, n + j) : 0.f;
+          for (int j = 0; j < 4; ++j) rb[i][j] = (k < kend && n + j < N) ? lb.at(k, n + j) : 0.f;
         }
-      }
-    } else {                                    // thread: one n, 8 consecutive k
-      const int n = n0 + (tid >> 1);
-      const int kb = k0 + (tid & 1) * 8;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int k = kb + 4 * h;
+      } else {                                  // column of 4 consecutive k
+        const int n = n0 + v / (DP_BK / 4), k = k0 + 4 * (v % (DP_BK / 4));
         if constexpr (LB::kVec) {
-          float4 v = (n < N && k < K) ? lb.at4(k, n) : make_float4(0.f, 0.f, 0.f, 0.f);
-          rb[4 * h + 0] = v.x; rb[4 * h + 1] = v.y; rb[4 * h + 2] = v.z; rb[4 * h + 3] = v.w;
+          const float4 x = (n < N && k < kend) ? lb.at4(k, n) : make_float4(0.f, 0.f, 0.f, 0.f);
+          rb[i][0] = x.x; rb[i][1] = x.y; rb[i][2] = x.z; rb[i][3] = x.w;
         } else {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) rb[4 * h + j] = (n < N && k + j < K) ? lb.at(k + j, n) : 0.f;
+          for (int j = 0; j < 4; ++j) rb[i][j] = (n < N && k + j < kend) ? lb.at(k + j, n) : 0.f;
         }
       }
     }
   };
   auto store_b = [&]() {
-    if constexpr (LB::kMode == 0) {
-      const int k = tid >> 4, nb = (tid & 15) * 8;
-      *reinterpret_cast<float4*>(&Bs[k][nb]) = make_float4(rb[0], rb[1], rb[2], rb[3]);
-      *reinterpret_cast<float4*>(&Bs[k][nb + 4]) = make_float4(rb[4], rb[5], rb[6], rb[7]);
-    } else {
-      const int n = tid >> 1, kb = (tid & 1) * 8;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) Bs[kb + j][n] = rb[j];
+    for (int i = 0; i < VB; ++i) {
+      const int v = tid + 256 * i;
+      if constexpr (LB::kMode == 0) {
+        const int k = v / (BN / 4), n = 4 * (v % (BN / 4));
+        *reinterpret_cast<float4*>(&Bs[k][n]) = make_float4(rb[i][0], rb[i][1], rb[i][2], rb[i][3]);
+      } else {
+        const int n = v / (DP_BK / 4), k = 4 * (v % (DP_BK / 4));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) Bs[k + j][n] = rb[i][j];
+      }
     }
   };
 
-  adhip_f32x16 acc[2][2];
+  adhip_f32x16 acc[TM][TN];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  load_a(0);
-  load_b(0);
-  store_a();
-  store_b();
-  __syncthreads();
   const int lk = lane >> 5, lr = lane & 31;
-  for (int k0 = 0; k0 < K; k0 += DP_BK) {
-    const bool more = k0 + DP_BK < K;
-    if (more) {
-      load_a(k0 + DP_BK);
-      load_b(k0 + DP_BK);
-    }
-#pragma unroll
-    for (int kk = 0; kk < DP_BK; kk += 2) {
-      const float a0 = As[kk + lk][wm * 64 + lr];
-      const float a1 = As[kk + lk][wm * 64 + 32 + lr];
-      const float b0 = Bs[kk + lk][wn * 64 + lr];
-      const float b1 = Bs[kk + lk][wn * 64 + 32 + lr];
-      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
-      acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
-      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
-      acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
-    }
+  if (kbeg < kend) {
+    load_a(kbeg);
+    load_b(kbeg);
+    store_a();
+    store_b();
     __syncthreads();
-    if (more) {
-      store_a();
-      store_b();
+    for (int k0 = kbeg; k0 < kend; k0 += DP_BK) {
+      const bool more = k0 + DP_BK < kend;
+      if (more) {
+        load_a(k0 + DP_BK);
+        load_b(k0 + DP_BK);
+      }
+#pragma unroll
+      for (int kk = 0; kk < DP_BK; kk += 2) {
+        float a[TM], b[TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) a[i] = As[kk + lk][wm * (BM / 2) + i * 32 + lr];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) b[j] = Bs[kk + lk][wn * (BN / 2) + j * 32 + lr];
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+      }
       __syncthreads();
+      if (more) {
+        store_a();
+        store_b();
+        __syncthreads();
+      }
     }
   }
   // 32x32 accumulator layout: lane holds column (lane % 32) and rows
   // 8*(r/4) + 4*(lane/32) + r%4 for r = 0..15
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
-        const int col = n0 + wn * 64 + j * 32 + lr;
-        if (row < M && col < N) epi(acc[i][j][r], row, col);
+        const int row = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+        const int col = n0 + wn * (BN / 2) + j * 32 + lr;
+        if (row < M && col < N) epi(acc[i][j][r], row, col, chunk);
       }
 }
 
 // ---------------------------------------------------------------- Reduce+Elw
 // LD::at(x, y) loads element y of reduced row x; LD::at4 four consecutive y.
 // LD::inc(y) is false for elements the reference's work-group tree drops.
+//
+// reduce_rows: one wave per row, four independent float4 streams per lane
+// (16 floats in flight), butterfly over the wave; lane 0 runs the epilogue.
 template <int OP, class LD, class EPI>
 __device__ __forceinline__ void reduce_rows(const LD& ld, const EPI& epi, unsigned V, unsigned R,
                                             bool pad_zero) {
   const unsigned lane = threadIdx.x & 63;
   const unsigned row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (row >= V) return;
-  float acc = OP == 0 ? 0.f : -__builtin_huge_valf();
+  const float id = OP == 0 ? 0.f : -__builtin_huge_valf();
+  float acc = id;
   if constexpr (LD::kVec) {
-    float acc2 = acc;
+    float a0 = id, a1 = id, a2 = id, a3 = id;
     unsigned y = lane * 4;
-    for (; y + 256 < R; y += 512) {
-      const float4 v = ld.at4(row, y);
-      const float4 w = ld.at4(row, y + 256);
-      acc = rop<OP>(rop<OP>(acc, v.x), v.y);
-      acc2 = rop<OP>(rop<OP>(acc2, v.z), v.w);
-      acc = rop<OP>(rop<OP>(acc, w.x), w.y);
-      acc2 = rop<OP>(rop<OP>(acc2, w.z), w.w);
+    for (; y + 768 < R; y += 1024) {
+      const float4 v0 = ld.at4(row, y);
+      const float4 v1 = ld.at4(row, y + 256);
+      const float4 v2 = ld.at4(row, y + 512);
+      const float4 v3 = ld.at4(row, y + 768);
+      a0 = rop<OP>(rop<OP>(rop<OP>(rop<OP>(a0, v0.x), v0.y), v0.z), v0.w);
+      a1 = rop<OP>(rop<OP>(rop<OP>(rop<OP>(a1, v1.x), v1.y), v1.z), v1.w);
+      a2 = rop<OP>(rop<OP>(rop<OP>(rop<OP>(a2, v2.x), v2.y), v2.z), v2.w);
+      a3 = rop<OP>(rop<OP>(rop<OP>(rop<OP>(a3, v3.x), v3.y), v3.z), v3.w);
     }
-    if (y < R) {
-      const float4 v = ld.at4(row, y);
-      acc = rop<OP>(rop<OP>(acc, v.x), v.y);
-      acc2 = rop<OP>(rop<OP>(acc2, v.z), v.w);
+    for (; y < R; y += 256) {
+      const float4 v0 = ld.at4(row, y);
+      a0 = rop<OP>(rop<OP>(rop<OP>(rop<OP>(a0, v0.x), v0.y), v0.z), v0.w);
     }
-    acc = rop<OP>(acc, acc2);
+    acc = rop<OP>(rop<OP>(a0, a1), rop<OP>(a2, a3));
   } else {
     for (unsigned y = lane; y < R; y += 64)
       if (ld.inc(y)) acc = rop<OP>(acc, ld.at(row, y));
@@ -213,25 +239,35 @@ __device__ __forceinline__ void reduce_rows(const LD& ld, const EPI& epi, unsign
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) acc = rop<OP>(acc, __shfl_xor(acc, off, 64));
   if (OP == 1 && pad_zero) acc = fmaxf(acc, 0.f);
-  if (lane == 0) epi(acc, row);
+  if (lane == 0) epi(acc, row, 0);
 }
 
-template <int OP, class LD, class EPI>
+// reduce_cols: 64 columns x 4 row groups per block, coalesced along the
+// columns, LDS combine.  SPLIT > 1 splits the rows into SPLIT chunks
+// (blockIdx.y) whose results go to the epilogue with the chunk index and
+// without the zero padding of MAX (applied once the chunks are combined).
+template <int OP, int SPLIT, class LD, class EPI>
 __device__ __forceinline__ void reduce_cols(const LD& ld, const EPI& epi, unsigned V, unsigned R,
                                             bool pad_zero) {
   __shared__ float part[4][64];
   const unsigned lane = threadIdx.x & 63, grp = threadIdx.x >> 6;
   const unsigned col = blockIdx.x * 64 + lane;
+  unsigned ybeg = 0, yend = R;
+  if constexpr (SPLIT > 1) {
+    const unsigned rc = (R + SPLIT - 1) / SPLIT;
+    ybeg = blockIdx.y * rc;
+    yend = ybeg + rc < R ? ybeg + rc : R;
+  }
   float acc = OP == 0 ? 0.f : -__builtin_huge_valf();
   if (col < V)
-    for (unsigned y = grp; y < R; y += 4)
+    for (unsigned y = ybeg + grp; y < yend; y += 4)
       if (ld.inc(y)) acc = rop<OP>(acc, ld.at(col, y));
   part[grp][lane] = acc;
   __syncthreads();
   if (grp == 0 && col < V) {
     acc = rop<OP>(rop<OP>(rop<OP>(part[0][lane], part[1][lane]), part[2][lane]), part[3][lane]);
-    if (OP == 1 && pad_zero) acc = fmaxf(acc, 0.f);
-    epi(acc, col);
+    if (SPLIT == 1 && OP == 1 && pad_zero) acc = fmaxf(acc, 0.f);
+    epi(acc, col, (int)blockIdx.y);
   }
 }
 

@@ -364,6 +364,16 @@ class Lowerer:
                 tid, off = n
                 lines.append(f"{self.params.ptr('scratch', 0, off)}[_global_id] = temp_{tid};")
                 continue
+            if kind == "sum":           # combine the chunk results of a split pass, in order
+                off, chunks, count, op, pad_zero = n
+                pp = self.params.ptr("scratch", 0, off)
+                lines.append(f"float _value = {pp}[_global_id];")
+                for c in range(1, chunks):
+                    nxt = f"{pp}[(unsigned long long)_global_id + {c * count}ull]"
+                    lines.append(f"_value = fmaxf(_value, {nxt});" if op else f"_value = _value + {nxt};")
+                if op and pad_zero:
+                    lines.append("_value = fmaxf(_value, 0.0f);")
+                continue
             value = self.rhs(kind, n, init_value)
             if n.kres.is_temp:
                 lines.append(f"temp_{n.kres.id} = {value};")
@@ -384,7 +394,7 @@ def _ity(bound) -> str:
 def _expr_bound(stmts, gmax, xmax, ymax):
     b = max(gmax, xmax, ymax, 1)
     for kind, n in stmts:
-        if kind in ("tmp", "load", "store"):
+        if kind in ("tmp", "load", "store", "sum"):
             continue
         ks = list(n.kargs) + ([n.kres] if not n.kres.is_none() else [])
         for k in ks:
@@ -418,6 +428,8 @@ def _vector_plan(stmts, n):
     if n % 4 != 0:
         return False
     for kind, node in stmts:
+        if kind == "sum":
+            return False
         if kind in ("tmp", "load", "store"):
             continue
         ks = list(node.kargs) + [node.kres]
@@ -435,7 +447,7 @@ def _vector_plan(stmts, n):
     return True
 
 
-def elementwise_plan(stmts, n, index_kind="global", n_cols=1, flops=0) -> KernelPlan:
+def elementwise_plan(stmts, n, index_kind="global", n_cols=1, flops=0, init_value=None) -> KernelPlan:
     """One thread per element (or per 4 elements when every access allows a
     float4), statements in order.  ``index_kind`` defines ``_x``/``_y`` for
     statements lifted out of a DotProd (``dp``: row = g / n_cols) or Reduce
@@ -452,7 +464,7 @@ def elementwise_plan(stmts, n, index_kind="global", n_cols=1, flops=0) -> Kernel
     vec = index_kind == "global" and _vector_plan(stmts, n)
     if not vec:
         low = Lowerer(ity, params)
-        body = "\n    ".join(low.statements(stmts, None))
+        body = "\n    ".join(low.statements(stmts, init_value))
         src = f"""extern "C" __global__ void __launch_bounds__({BLOCK}) {KNAME}({_params_decl(params)}{', ' if params.slots else ''}unsigned long long n_) {{
   const {ity} _global_id = ({ity})blockIdx.x * {BLOCK}u + threadIdx.x;
   if (_global_id >= ({ity})n_) return;
@@ -589,7 +601,10 @@ def _loader_struct(name, karg, role, params: Params, ity, dims) -> Tuple[str, bo
                 f"  __device__ float4 at4({ity}, {ity}) const {{ return make_float4(0.f, 0.f, 0.f, 0.f); }} }};\n"), False
     assert isinstance(karg, KMatrix) and not karg.is_temp, "DotProd operand must be a buffer or constant"
     core, c = split_const(karg.access)
-    p = params.ptr("buf", karg.id, c)
+    if getattr(karg, "scratch_offset", None) is not None:
+        p = params.ptr("scratch", 0, karg.scratch_offset + c)
+    else:
+        p = params.ptr("buf", karg.id, c)
     idx = lower_index(core, ity)
     # A: mode 0 contiguous along k (= _y); B: mode 0 contiguous along n (= _y)
     vy = vec_class(core, Y)
@@ -618,26 +633,50 @@ def _init_list(params: Params) -> str:
     return ", ".join(f"p{i}" for i in range(len(params.slots)))
 
 
-def dotprod_plan(stmts, dp, flops_only=False) -> KernelPlan:
+def dp_config(M, N, K):
+    """Block tile and K split of a DotProd: 64-wide tiles on a narrow side,
+    128 otherwise; K is split (up to 16 chunks of at least 256) while the
+    tiles alone would not give one block per compute unit."""
+    BM = 64 if M <= 64 else 128
+    BN = 64 if N <= 64 else 128
+    tiles = ceil(M / BM) * ceil(N / BN)
+    split = 1
+    while tiles * split < 256 and split < 16 and K // (2 * split) >= 256:
+        split *= 2
+    return BM, BN, split
+
+
+def dotprod_plan(stmts, dp, A=None, B=None, config=None, partial_off=None) -> KernelPlan:
     """DotProd (+ elementwise epilogue) on fp32 MFMA tiles
-    (kernels/dotprod.py:7-43, dp_elw_fuse.py:26-65 semantics)."""
+    (kernels/dotprod.py:7-43, dp_elw_fuse.py:26-65 semantics).  ``A``/``B``
+    replace the node's operands (a gathered copy in scratch); with a K split
+    (``config[2] > 1``) the blocks store partial products to scratch at
+    ``partial_off`` ([chunk][M][N]) and ``stmts`` must be empty."""
     M, N = dp.shape
     K = dp.children_shapes[0][1]
+    BM, BN, split = config if config is not None else dp_config(M, N, K)
+    A = dp.kargs[0] if A is None else A
+    B = dp.kargs[1] if B is None else B
     bound = _expr_bound(stmts, M * N, max(M, K), max(N, K))
     ity = _ity(bound)
     params = Params()
-    la, _ = _loader_struct("LA", dp.kargs[0], "A", params, ity, (M, K))
-    lb, _ = _loader_struct("LB", dp.kargs[1], "B", params, ity, (K, N))
-    low = Lowerer(ity, params)
-    body = "\n    ".join(low.statements(stmts, "_value"))
+    la, _ = _loader_struct("LA", A, "A", params, ity, (M, K))
+    lb, _ = _loader_struct("LB", B, "B", params, ity, (K, N))
+    if split > 1:
+        assert not stmts, "a split DotProd stores partial products only"
+        pp = params.ptr("scratch", 0, partial_off)
+        body = (f"{pp}[((unsigned long long)_chunk * {M}ull + _x) * {N}ull + _y] = _value;")
+    else:
+        low = Lowerer(ity, params)
+        body = "\n    ".join(low.statements(stmts, "_value"))
     epi = (f"struct EPI {{ @FIELDS@\n"
-           f"  __device__ void operator()(float _value, {ity} _x, {ity} _y) const {{\n"
-           f"    const {ity} _global_id = _x * ({ity}){N} + _y; (void)_global_id;\n    {body}\n  }} }};\n")
+           f"  __device__ void operator()(float _value, {ity} _x, {ity} _y, int _chunk) const {{\n"
+           f"    const {ity} _global_id = _x * ({ity}){N} + _y; (void)_global_id; (void)_chunk;\n    {body}\n  }} }};\n")
     init = _init_list(params)
     src = ((la + lb + epi).replace("@FIELDS@", _fields(params)) +
            f"extern \"C\" __global__ void __launch_bounds__(256) {KNAME}({_params_decl(params)}) {{\n"
-           f"  adhip::dp_mfma(LA{{{init}}}, LB{{{init}}}, EPI{{{init}}}, {M}, {N}, {K});\n}}\n")
-    grid = (ceil(N / 128), ceil(M / 128), 1)
+           f"  adhip::dp_mfma<{BM}, {BN}, {split}>(LA{{{init}}}, LB{{{init}}}, EPI{{{init}}}, {M}, {N}, {K});\n}}\n")
+    grid = (ceil(N / BN), ceil(M / BM) * split, 1)
     return KernelPlan(src, grid, (256, 1, 1), _plan_args(params), family="dotprod",
                       flops=2 * M * N * K)
 
@@ -659,9 +698,28 @@ def tree_inclusion(R):
     return sorted(sets[0])
 
 
-def reduce_plan(stmts, red) -> KernelPlan:
+def reduce_mode(red):
+    """``("rows"|"cols", split)`` for a Reduce: rows when the reduced axis is
+    contiguous, cols when the kept axis is; columns are split over blocks
+    when too few column blocks would fill the device."""
+    V, R = red.children_shapes[0]
+    karg = red.kargs[0]
+    if isinstance(karg, KMatrix):
+        core, _ = split_const(karg.access)
+        if vec_class(core, Y).kind != AFF and vec_class(core, X).kind == AFF:
+            blocks = ceil(V / 64)
+            split = 1
+            while blocks * split < 512 and split < 64 and R // (2 * split) >= 64:
+                split *= 2
+            return "cols", split
+    return "rows", 1
+
+
+def reduce_plan(stmts, red, partial_off=None) -> KernelPlan:
     """Row reduction (+ epilogue on the reduced value)
-    (kernels/reduce.py:8-66, reduce_elw_fuse.py:12-80 semantics)."""
+    (kernels/reduce.py:8-66, reduce_elw_fuse.py:12-80 semantics).  When the
+    columns are split, the blocks store partial results to scratch at
+    ``partial_off`` ([chunk][V]) and ``stmts`` must be empty."""
     V, R = red.children_shapes[0]
     inc = tree_inclusion(R)
     dropped = [y for y in range(R) if y not in set(inc)] if len(inc) < R else []
@@ -670,7 +728,7 @@ def reduce_plan(stmts, red) -> KernelPlan:
     ity = _ity(bound)
     params = Params()
     karg = red.kargs[0]
-    mode = "rows"
+    mode, split = reduce_mode(red)
     vec = False
     if isinstance(karg, KConstant):
         at = f"return (float)({const_literal(karg.constant)});"
@@ -687,11 +745,8 @@ def reduce_plan(stmts, red) -> KernelPlan:
             at = f"return {p}[{idx}];"
             at4 = f"return *reinterpret_cast<const float4*>({p} + {idx});"
             vy = vec_class(core, Y)
-            vx = vec_class(core, X)
             if vy.kind == AFF:
                 vec = vy.al and c % 4 == 0 and R % 4 == 0 and not dropped
-            elif vx.kind == AFF:
-                mode = "cols"
     if dropped:
         words = [0] * ((R + 31) // 32)
         for y in inc:
@@ -705,18 +760,24 @@ def reduce_plan(stmts, red) -> KernelPlan:
     ld = (f"struct LD {{ static constexpr bool kVec = {'true' if vec else 'false'}; @FIELDS@\n"
           f"  __device__ float at({ity} _x, {ity} _y) const {{ (void)_x; (void)_y; {at} }}\n"
           f"  __device__ float4 at4({ity} _x, {ity} _y) const {{ (void)_x; (void)_y; {at4} }}\n{inc_fn}}};\n")
-    low = Lowerer(ity, params)
-    body = "\n    ".join(low.statements(stmts, "_v"))
+    if split > 1:
+        assert not stmts, "a split Reduce stores partial results only"
+        pp = params.ptr("scratch", 0, partial_off)
+        body = f"{pp}[(unsigned long long)_chunk * {V}ull + _x] = _v;"
+    else:
+        low = Lowerer(ity, params)
+        body = "\n    ".join(low.statements(stmts, "_v"))
     epi = (f"struct EPI {{ @FIELDS@\n"
-           f"  __device__ void operator()(float _v, {ity} _x) const {{\n"
-           f"    const {ity} _y = 0; const {ity} _global_id = _x; (void)_y; (void)_global_id;\n    {body}\n  }} }};\n")
+           f"  __device__ void operator()(float _v, {ity} _x, int _chunk) const {{\n"
+           f"    const {ity} _y = 0; const {ity} _global_id = _x; (void)_y; (void)_global_id; (void)_chunk;\n"
+           f"    {body}\n  }} }};\n")
     op = 0 if red.op == ReduceOp.SUM else 1
     init = _init_list(params)
-    fn = "reduce_rows" if mode == "rows" else "reduce_cols"
+    call = (f"adhip::reduce_rows<{op}>" if mode == "rows" else f"adhip::reduce_cols<{op}, {split}>")
     src = ((ld + epi).replace("@FIELDS@", _fields(params)) +
            f"extern \"C\" __global__ void __launch_bounds__(256) {KNAME}({_params_decl(params)}) {{\n"
-           f"  adhip::{fn}<{op}>(LD{{{init}}}, EPI{{{init}}}, {V}u, {R}u, {'true' if pad_zero else 'false'});\n}}\n")
-    grid = (ceil(V / 4), 1, 1) if mode == "rows" else (ceil(V / 64), 1, 1)
+           f"  {call}(LD{{{init}}}, EPI{{{init}}}, {V}u, {R}u, {'true' if pad_zero else 'false'});\n}}\n")
+    grid = (ceil(V / 4), 1, 1) if mode == "rows" else (ceil(V / 64), split, 1)
     return KernelPlan(src, grid, (256, 1, 1), _plan_args(params), family="reduce",
                       bytes=4 * V * R + 4 * V)
 
@@ -729,23 +790,14 @@ def lockstep_plans(stmts, n, index_kind, n_cols, init_node, scratch_base):
     the DotProd/Reduce value live in scratch arrays.  Returns (plans,
     scratch floats used)."""
     temps = [node.id for kind, node in stmts if kind == "tmp"]
-    off = scratch_base
-    temp_off = {}
-    for t in temps:
-        temp_off[t] = off
-        off += n
-    stage_off = off
-    off += n
-    init_off = off
-    off += n
+    alloc = ScratchAlloc(scratch_base)
+    temp_off = {t: alloc.take(n) for t in temps}
+    stage_off = alloc.take(n)
+    init_off = alloc.take(n)
     plans = []
     if init_node is not None:
         sink = _scratch_km(init_off, _identity_access(index_kind, n_cols))
-        fake = _ValueSink(sink)
-        if isinstance(init_node, DotProdNode):
-            plans.append(dotprod_plan([("init", fake)], init_node))
-        else:
-            plans.append(reduce_plan([("init", fake)], init_node))
+        plans.extend(first_pass_plans([("init", _ValueSink(sink))], n, init_node, alloc))
     for kind, node in stmts:
         if kind == "tmp":
             continue
@@ -753,7 +805,7 @@ def lockstep_plans(stmts, n, index_kind, n_cols, init_node, scratch_base):
                                 to_stage=True))
         plans.append(_stmt_plan(kind, node, n, index_kind, n_cols, temp_off, stage_off, init_off,
                                 to_stage=False))
-    return plans, off - scratch_base
+    return plans, alloc.used
 
 
 def _identity_access(index_kind, n_cols):
@@ -838,19 +890,92 @@ def command_plans(cmd, buffers: BufferInfo, scratch_base: int):
         raise TypeError(f"Encountered unexpected cmd: {cmd}")
 
     pairs = conflict_pairs(stmts, buffers, kind, cols)
-    if not pairs:
-        return single_pass_plans(stmts, n, init), 0, False
     if any(i == j for i, j in pairs):
         return lockstep_plans(stmts, n, kind, cols, init, scratch_base) + (True,)
-    return phased_plans(stmts, pairs, n, kind, cols, init, scratch_base) + (True,)
+    plans, need = phased_plans(stmts, pairs, n, kind, cols, init, scratch_base)
+    return plans, need, len(plans) > 1
 
 
-def single_pass_plans(stmts, n, init):
-    if isinstance(init, DotProdNode):
-        return [dotprod_plan(stmts, init)]
-    if isinstance(init, ReduceNode):
-        return [reduce_plan(stmts, init)]
-    return [elementwise_plan(stmts, n)]
+class ScratchAlloc:
+    """Bump allocator over a command's scratch floats (64-float aligned)."""
+
+    def __init__(self, base=0):
+        self.base = base
+        self.end = base
+
+    def take(self, nfloats):
+        off = self.end
+        self.end += (nfloats + 63) // 64 * 64
+        return off
+
+    @property
+    def used(self):
+        return self.end - self.base
+
+
+class _Stmt:
+    """A generated statement ``kres = kargs[0]`` (an operand gather)."""
+
+    def __init__(self, kargs, kres):
+        self.kargs = kargs
+        self.kres = kres
+
+
+# a DotProd operand given as a concat of matrices (nested conditions per
+# element) is first gathered into a dense scratch copy when the product is
+# at least this many multiply-adds
+GATHER_MIN_MACS = 1 << 22
+
+
+def gather_plan(karg, rows, cols, dst_off) -> KernelPlan:
+    """Dense row-major copy ``scratch[r * cols + c] = operand(r, c)`` of a
+    DotProd operand in the (_x, _y) convention of its kernel arg."""
+    sink = _scratch_km(dst_off, Global())
+    return elementwise_plan([("copy", _Stmt([karg], sink))], rows * cols, index_kind="dp", n_cols=cols)
+
+
+def _dense_scratch_operand(off, cols):
+    return _scratch_km(off, Add(Mult(X(), Val(Constant(cols))), Y()))
+
+
+def first_pass_plans(part, n, init_node, alloc: ScratchAlloc):
+    """Plans of the pass that runs the DotProd or Reduce of a command with
+    ``part`` as its epilogue: operand gathers, then the product (or the
+    reduction) with the epilogue in registers, or -- split over K / rows --
+    partial results followed by an elementwise pass that combines them in
+    chunk order and runs the epilogue."""
+    if isinstance(init_node, DotProdNode):
+        M, N = init_node.shape
+        K = init_node.children_shapes[0][1]
+        cfg = dp_config(M, N, K)
+        A, B = init_node.kargs
+        pre = []
+        if isinstance(A, KConcat) and M * N * K >= GATHER_MIN_MACS:
+            off = alloc.take(M * K)
+            pre.append(gather_plan(A, M, K, off))
+            A = _dense_scratch_operand(off, K)
+        if isinstance(B, KConcat) and M * N * K >= GATHER_MIN_MACS:
+            off = alloc.take(K * N)
+            pre.append(gather_plan(B, K, N, off))
+            B = _dense_scratch_operand(off, N)
+        if cfg[2] == 1:
+            return pre + [dotprod_plan(part, init_node, A, B, cfg)]
+        poff = alloc.take(cfg[2] * M * N)
+        main = dotprod_plan([], init_node, A, B, cfg, partial_off=poff)
+        comb = elementwise_plan([("sum", (poff, cfg[2], M * N, 0, False))] + part, M * N,
+                                index_kind="dp", n_cols=N, init_value="_value")
+        return pre + [main, comb]
+    mode, split = reduce_mode(init_node)
+    if split == 1:
+        return [reduce_plan(part, init_node)]
+    V, R = init_node.children_shapes[0]
+    pad_zero = any(y >= R for y in tree_inclusion(R))
+    poff = alloc.take(split * V)
+    main = reduce_plan([], init_node, partial_off=poff)
+    op = 0 if init_node.op == ReduceOp.SUM else 1
+    comb = elementwise_plan([("sum", (poff, split, V, op, pad_zero))] + part, V,
+                            index_kind="red", init_value="_value")
+    return [main, comb]
 
 
 def split_phases(n_stmts, pairs):
@@ -888,7 +1013,7 @@ def _temp_uses(stmts):
     return reads, assigns
 
 
-def phased_plans(stmts, pairs, n, index_kind, n_cols, init_node, scratch_base):
+def phased_plans(stmts, pairs, n, index_kind, n_cols, init_node, scratch_base=0):
     """A command whose statements conflict across elements, run as several
     passes over the elements (one kernel each): the first pass is the
     DotProd/Reduce (if any) with the statements up to the first conflict in
@@ -909,13 +1034,11 @@ def phased_plans(stmts, pairs, n, index_kind, n_cols, init_node, scratch_base):
         for tid in rs:
             used_in.setdefault(tid, set()).add(phase_of_stmt[si])
     # scratch slot per temp that crosses a pass boundary
+    alloc = ScratchAlloc(scratch_base)
     slot = {}
-    off = scratch_base
-    stride = (n + 63) // 64 * 64
     for tid, pa in sorted(assigned_in.items()):
         if any(pu > pa for pu in used_in.get(tid, ())):
-            slot[tid] = off
-            off += stride
+            slot[tid] = alloc.take(n)
     plans = []
     for pi, (a, b) in enumerate(phases):
         body = [st for st in stmts[a:b] if st[0] != "tmp"]
@@ -933,8 +1056,8 @@ def phased_plans(stmts, pairs, n, index_kind, n_cols, init_node, scratch_base):
         tail = [("store", (tid, slot[tid])) for tid in sorted(slot) if assigned_in[tid] == pi]
         part = head + body + tail
         if pi == 0 and init_node is not None:
-            plans.extend(single_pass_plans(part, n, init_node))
+            plans.extend(first_pass_plans(part, n, init_node, alloc))
         else:
             kind = "global" if init_node is None else ("dp" if isinstance(init_node, DotProdNode) else "red")
             plans.append(elementwise_plan(part, n, index_kind=kind, n_cols=n_cols))
-    return plans, off - scratch_base
+    return plans, alloc.used

@@ -39,6 +39,7 @@ from .runtime import HEADER_PATH, Context, compile_source
 from .schedule import schedule
 
 ALIGN = 256
+SCRATCH_RING_FLOATS = 64 << 20     # 256 MiB of scratch slots for multi-pass commands
 _code_cache = {}            # source text -> code object (process-wide)
 _code_lock = threading.Lock()
 
@@ -125,21 +126,33 @@ class HIPDevice(Device):
         for fid in list(self._feeder_slots):
             self._feeder_slots[fid] = off
             off += _align(self._feeder_size.get(fid, 0) * 4)
-        # kernel plans and the ranges each command touches
-        scratch_need = 0
-        plans, regions = {}, {}
+        # kernel plans and the ranges each command touches; commands that need
+        # scratch get consecutive slots of a ring, so neighbouring commands do
+        # not share scratch and can run in one launch
+        plans, regions, needs = {}, {}, {}
         for cmd in self._pending:
             ps, need, multipass = codegen.command_plans(cmd, info, 0)
             plans[cmd.program_id] = ps
-            reads, writes = codegen.command_regions(cmd, info)
-            if need:
-                reads.append(("scratch", 0, need))
-                writes.append(("scratch", 0, need))
-            regions[cmd.program_id] = (reads, writes)
-            scratch_need = max(scratch_need, need)
+            needs[cmd.program_id] = (need + 63) // 64 * 64
+            regions[cmd.program_id] = codegen.command_regions(cmd, info)
             self.stats["multipass_cmds"] += int(multipass)
+        max_need = max(needs.values(), default=0)
+        ring = max(max_need, min(sum(needs.values()), SCRATCH_RING_FLOATS))
+        self._scratch_base = {}
+        cursor = 0
+        for cmd in self._pending:
+            need = needs[cmd.program_id]
+            if need == 0:
+                continue
+            if cursor + need > ring:
+                cursor = 0
+            self._scratch_base[cmd.program_id] = cursor
+            reads, writes = regions[cmd.program_id]
+            reads.append(("scratch", cursor, cursor + need))
+            writes.append(("scratch", cursor, cursor + need))
+            cursor += need
         self.scratch_off = off
-        off += _align(scratch_need * 4)
+        off += _align(ring * 4)
         # schedule every stretch of every Proc, then lay out argument tables
         rows = []                      # (byte offset in table region, [u64 values])
         table_bytes = [0]
@@ -154,7 +167,7 @@ class HIPDevice(Device):
         self._plans = plans
         launch_rows = {}               # program_id -> [row offsets per plan]
         for pid, ps in plans.items():
-            launch_rows[pid] = [add_rows([self._arg_values(p)]) for p in ps]
+            launch_rows[pid] = [add_rows([self._arg_values(p, pid)]) for p in ps]
         sched = self._build_schedules(proc, plans, regions, add_rows)
         self.table_off = off
         off += _align(max(table_bytes[0], 8))
@@ -190,16 +203,16 @@ class HIPDevice(Device):
             self._schedules[pid_proc] = out
         self._pending = []
 
-    def _arg_values(self, plan):
-        """Argument row of a plan: ``(True, arena byte offset)`` for a pointer
-        (resolved against the arena base once it exists), ``(False, v)`` for
-        an integer."""
+    def _arg_values(self, plan, pid):
+        """Argument row of a plan of command ``pid``: ``(True, arena byte
+        offset)`` for a pointer (resolved against the arena base once it
+        exists), ``(False, v)`` for an integer."""
         vals = []
         for a in plan.args:
             if a[0] == "buf":
                 vals.append((True, self.buffers[a[1]] + 4 * a[2]))
             elif a[0] == "scratch":
-                vals.append((True, self.scratch_off + 4 * a[1]))
+                vals.append((True, self.scratch_off + 4 * (self._scratch_base[pid] + a[1])))
             else:
                 vals.append((False, int(a[1]) & 0xFFFFFFFFFFFFFFFF))
         return vals
@@ -226,7 +239,7 @@ class HIPDevice(Device):
                 for group in schedule([(L, L.reads, L.writes) for L in launches], key):
                     members = [launches[i] for i in group]
                     plan = members[0].plan
-                    row = add_rows([self._arg_values(m.plan) for m in members])
+                    row = add_rows([self._arg_values(m.plan, m.cmd.program_id) for m in members])
                     items.append(("launch", plan, row, len(members)))
                 stretch.clear()
 

@@ -152,3 +152,73 @@ def test_layernorm_wide_parity(hip):
     from ad_amd import workloads
     a, b = run_both(lambda: workloads.layernorm_train(rows=64, cols=1024, steps=2), hip)
     assert_params_close(a, b)
+
+
+@pytest.mark.parametrize("M,K,N", [(128, 4096, 64), (64, 2048, 64), (1024, 4096, 64), (256, 1024, 256)])
+@pytest.mark.parametrize("ta", [False, True])
+def test_dotprod_split_k(hip, M, K, N, ta):
+    """Few output tiles and a long K: the product is split over K into
+    partial products combined in chunk order (then +bias, sigmoid)."""
+    from ad_amd.device.hip.codegen import dp_config
+    assert dp_config(M, N, K)[2] > 1
+    rng = np.random.default_rng(M + K + N)
+    a = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    b = rng.standard_normal((K, N)).astype(np.float32)
+    bias = rng.standard_normal((N,)).astype(np.float32)
+    A = Tensor(a)
+    r = ((A.T() if ta else A) @ Tensor(b)) + Tensor(bias)
+    got = {}
+    Receiver(lambda v: got.setdefault("r", v.copy()), [r])
+    ad.execute(device=hip())
+    ref = (a.T if ta else a).astype(np.float64) @ b.astype(np.float64) + bias
+    bound = 4 * K * np.finfo(np.float32).eps * (np.abs(a).max() * np.abs(b).max()) + 1e-5
+    np.testing.assert_allclose(got["r"], ref, rtol=0, atol=bound)
+
+
+def test_dotprod_concat_operands(hip):
+    """Operands given as concats (rows of A, columns of B) are gathered into
+    dense scratch copies before the MFMA product."""
+    from ad_amd.device.hip.codegen import GATHER_MIN_MACS
+    rng = np.random.default_rng(7)
+    parts_a = [rng.standard_normal((128, 256)).astype(np.float32) for _ in range(3)]
+    parts_b = [rng.standard_normal((256, 64)).astype(np.float32) for _ in range(2)]
+    A = ad.concat([Tensor(x) for x in parts_a], 0)
+    B = ad.concat([Tensor(x) for x in parts_b], 1)
+    assert 384 * 256 * 128 >= GATHER_MIN_MACS
+    r = A @ B
+    got = {}
+    Receiver(lambda v: got.setdefault("r", v.copy()), [r])
+    ad.execute(device=hip())
+    a = np.concatenate(parts_a, 0).astype(np.float64)
+    b = np.concatenate(parts_b, 1).astype(np.float64)
+    bound = 4 * 256 * np.finfo(np.float32).eps * (np.abs(a).max() * np.abs(b).max())
+    np.testing.assert_allclose(got["r"], a @ b, rtol=0, atol=bound)
+
+
+@pytest.mark.parametrize("rows,cols", [(4096, 256), (16384, 64), (1000, 100)])
+def test_column_reduce_split(hip, rows, cols):
+    """Reductions over rows of a row-major matrix (bias / LayerNorm gradient
+    shape): split over blocks of rows, combined in order; SUM and MAX."""
+    rng = np.random.default_rng(rows + cols)
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    X = Tensor(x)
+    s = X.sum(0) * 0.5
+    m = X.max(0)
+    got = {}
+    Receiver(lambda a, b: got.update(s=a.copy(), m=b.copy()), [s, m])
+    ad.execute(device=hip())
+    if rows & (rows - 1) == 0:
+        # a power-of-two tree sums every element
+        np.testing.assert_allclose(got["s"], 0.5 * x.astype(np.float64).sum(0),
+                                   rtol=0, atol=rows * np.finfo(np.float32).eps * 4)
+    # otherwise the reference's tree drops elements (and MAX pads with 0):
+    # compare with the oracle, which restates that tree
+    ad.reset()
+    X = Tensor(x)
+    s = X.sum(0) * 0.5
+    m = X.max(0)
+    want = {}
+    Receiver(lambda a, b: want.update(s=a.copy(), m=b.copy()), [s, m])
+    ad.execute(device=OracleDevice())
+    np.testing.assert_allclose(got["s"], want["s"], rtol=1e-4, atol=1e-4)
+    assert np.array_equal(got["m"], want["m"])
