@@ -37,7 +37,7 @@ __device__ __forceinline__ float rop(float a, float b) {
 // SPLIT > 1 splits K into SPLIT chunks: blockIdx.y = tile row + tiles_m *
 // chunk, and the epilogue receives the chunk index (partial results).
 // The epilogue is called as epi(value, row, col, chunk) in registers.
-constexpr int DP_BK = 16, DP_PAD = 4;
+constexpr int DP_BK = 16, DP_PAD = 4, DP_GROUP = 8;
 
 template <int BM, int BN, int SPLIT, class LA, class LB, class EPI>
 __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& epi, int M, int N, int K) {
@@ -53,9 +53,22 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
   const int wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int tiles_m = (M + BM - 1) / BM;
-  const int by = blockIdx.y;
+  int bx = blockIdx.x, by = blockIdx.y;
+  {
+    // Workgroups go to the 8 XCDs round-robin, each XCD with its own L2:
+    // give every XCD a contiguous run of tiles, ordered in groups of
+    // DP_GROUP tile rows, so blocks sharing A rows and B columns share an L2.
+    const int gx = gridDim.x, gy = gridDim.y, T = gx * gy;
+    int L = by * gx + bx;
+    if (T % 8 == 0) L = (L % 8) * (T / 8) + L / 8;
+    const int per_group = DP_GROUP * gx;
+    const int first = (L / per_group) * DP_GROUP;
+    const int rows = gy - first < DP_GROUP ? gy - first : DP_GROUP;
+    by = first + (L % per_group) % rows;
+    bx = (L % per_group) / rows;
+  }
   const int chunk = SPLIT > 1 ? by / tiles_m : 0;
-  const int m0 = (SPLIT > 1 ? by % tiles_m : by) * BM, n0 = blockIdx.x * BN;
+  const int m0 = (SPLIT > 1 ? by % tiles_m : by) * BM, n0 = bx * BN;
   int kbeg = 0, kend = K;
   if constexpr (SPLIT > 1) {
     const int kc = ((K + SPLIT - 1) / SPLIT + DP_BK - 1) / DP_BK * DP_BK;

@@ -133,22 +133,26 @@ class VC:
         self.al = al
 
 
-def vec_class(e, var_type):
+def vec_class(e, var_type, zero=()):
     """Classify ``e`` as a function of the index variable of type
-    ``var_type`` (Global, X or Y); the other index variables are arbitrary
-    per group (INV, unknown residue)."""
+    ``var_type`` (Global, X or Y, or a tuple of types that all advance with
+    the element index); variables whose type is in ``zero`` are 0; the other
+    index variables are arbitrary per group (INV, unknown residue)."""
     c = const_of(e)
     if c is not None:
         return VC(INV, c % 4 == 0)
     if isinstance(e, (Global, X, Y)):
-        return VC(AFF, True) if type(e) is var_type else VC(INV, False)
+        if type(e) in zero:
+            return VC(INV, True)
+        moving = type(e) in var_type if isinstance(var_type, tuple) else type(e) is var_type
+        return VC(AFF, True) if moving else VC(INV, False)
     if type(e) is Val:
-        return vec_class(e.v, var_type)
+        return vec_class(e.v, var_type, zero)
     t = type(e)
-    a = vec_class(e.a, var_type)
+    a = vec_class(e.a, var_type, zero)
     kb = const_of(e.b)
     if t in (Add, Minus):
-        b = vec_class(e.b, var_type)
+        b = vec_class(e.b, var_type, zero)
         if a.kind == AFF and b.kind == INV:
             return VC(AFF, a.al and b.al)
         if t is Add and a.kind == INV and b.kind == AFF:
@@ -157,7 +161,7 @@ def vec_class(e, var_type):
             return VC(INV, a.al and b.al)
         return VC(UNK)
     if t is Mult:
-        b = vec_class(e.b, var_type)
+        b = vec_class(e.b, var_type, zero)
         if a.kind == INV and b.kind == INV:
             return VC(INV, a.al or b.al)
         if a.kind == AFF and kb == 1:
@@ -207,12 +211,12 @@ def vec_class(e, var_type):
                 return VC(INV, False)
         return VC(UNK)
     if t in (MoreThan, LessThan):
-        b = vec_class(e.b, var_type)
+        b = vec_class(e.b, var_type, zero)
         if a.kind == INV and b.kind == INV:
             return VC(INV, False)
         return VC(UNK)
     # other operators with a non-constant right operand
-    b = vec_class(e.b, var_type)
+    b = vec_class(e.b, var_type, zero)
     if a.kind == INV and b.kind == INV:
         return VC(INV, False)
     return VC(UNK)

@@ -53,6 +53,9 @@ class KernelPlan:
     bytes: int = 0                # algorithmic bytes for reporting
 
     name: str = ""                # kernel symbol: adhip_<family>_<hash of the source>
+    reads: Optional[list] = None  # ranges read / written, when narrower than the command's
+    writes: Optional[list] = None
+    scratch: Tuple[int, int] = (0, 0)   # [lo, hi) of the command's scratch floats it touches
 
     def __post_init__(self):
         # register temps are named after node ids; number them by first use
@@ -211,14 +214,13 @@ def conflict_pairs(stmts, buffers: BufferInfo, index_kind: str, n_cols: int = 1)
     return sorted(out)
 
 
-def command_regions(cmd, buffers: BufferInfo):
-    """Buffer ranges ``(buffer, lo, hi)`` (floats) a command may read and may
-    write: the packed region of each arena variable it addresses, or the
-    whole buffer otherwise."""
-    nodes = cmd.nodes if hasattr(cmd, "nodes") else [cmd]
+def stmt_regions(stmts, buffers: BufferInfo):
+    """Buffer ranges ``(buffer, lo, hi)`` (floats) a statement list may read
+    and may write: the packed region of each arena variable it addresses, or
+    the whole buffer otherwise."""
     reads, writes = set(), set()
-    for kind, n in statements(nodes):
-        if kind == "tmp":
+    for kind, n in stmts:
+        if kind in ("tmp", "load", "store", "sum"):
             continue
         for k in n.kargs:
             for km in _iter_kmatrix(k):
@@ -227,6 +229,85 @@ def command_regions(cmd, buffers: BufferInfo):
         if not n.kres.is_none() and not n.kres.is_temp:
             writes.add(_region(n.kres, buffers)[0])
     return sorted(reads, key=repr), sorted(writes, key=repr)
+
+
+def command_regions(cmd, buffers: BufferInfo):
+    nodes = cmd.nodes if hasattr(cmd, "nodes") else [cmd]
+    return stmt_regions(statements(nodes), buffers)
+
+
+def components(stmts, buffers: BufferInfo):
+    """Split an elementwise statement list into groups that share no temp
+    and no memory range one of them writes; each group keeps its statements
+    in order.  Groups are independent: any order of running them (or running
+    them at once) gives the result of the whole list."""
+    parent = list(range(len(stmts)))
+
+    def find(i):
+        while parent[i] != i:
+            parent[i] = parent[parent[i]]
+            i = parent[i]
+        return i
+
+    def union(i, j):
+        ri, rj = find(i), find(j)
+        if ri != rj:
+            parent[max(ri, rj)] = min(ri, rj)
+
+    defined, decl = {}, {}
+    accesses = {}
+    for i, (kind, n) in enumerate(stmts):
+        if kind == "tmp":
+            decl[n.id] = i
+            continue
+        if not n.kres.is_none() and n.kres.is_temp:
+            defined[n.kres.id] = i
+    for i, (kind, n) in enumerate(stmts):
+        if kind == "tmp":
+            continue
+        for k in n.kargs:
+            for km in _iter_kmatrix(k):
+                if km.is_temp:
+                    j = defined.get(km.id, decl.get(km.id))
+                    if j is not None:
+                        union(i, j)
+                else:
+                    (buf, lo, hi), _ = _region(km, buffers)
+                    accesses.setdefault(buf, []).append((lo, hi, i, False))
+        if not n.kres.is_none():
+            if n.kres.is_temp:
+                if n.kres.id in decl:
+                    union(i, decl[n.kres.id])
+            else:
+                (buf, lo, hi), _ = _region(n.kres, buffers)
+                accesses.setdefault(buf, []).append((lo, hi, i, True))
+    # sweep each buffer's accesses by start: a write joins every live access
+    # it overlaps.  All live writes are already joined, so the one reaching
+    # furthest stands for them; reads since the last write are kept until the
+    # next write joins (and so merges) the live ones.
+    for buf, acc in accesses.items():
+        acc.sort(key=lambda a: (a[0], a[1]))
+        write_rep = None           # (hi, stmt) of the furthest-reaching live write
+        reads = []                 # reads not yet merged by a write: (hi, stmt)
+        for lo, hi, i, is_write in acc:
+            if hi <= lo:
+                continue
+            if write_rep is not None and write_rep[0] <= lo:
+                write_rep = None
+            if write_rep is not None:
+                union(i, write_rep[1])
+            if is_write:
+                live = [r for r in reads if r[0] > lo]
+                for _, j in live:
+                    union(i, j)
+                reads = [max(live)] if live else []
+                write_rep = (hi, i) if write_rep is None or hi > write_rep[0] else write_rep
+            else:
+                reads.append((hi, i))
+    groups = {}
+    for i in range(len(stmts)):
+        groups.setdefault(find(i), []).append(stmts[i])
+    return [groups[r] for r in sorted(groups)]
 
 
 def hazards(stmts, buffers: BufferInfo, index_kind: str, n_cols: int = 1) -> bool:
@@ -421,30 +502,60 @@ KNAME = "adhip_kernel"
 
 
 # ------------------------------------------------------------------ ElwFuse family
-def _vector_plan(stmts, n):
-    """Lane layout for 4 elements per thread: every non-temp access must be
-    contiguous-aligned or constant over aligned groups of 4, with its folded
-    offset a multiple of 4 floats."""
-    if n % 4 != 0:
+def _moving(index_kind):
+    """Index variables that advance with the element index inside an aligned
+    group of 4 elements, and those that are 0, per element space."""
+    if index_kind == "dp":
+        return (Global, Y), ()            # valid when the row length is a multiple of 4
+    if index_kind == "red":
+        return (Global, X), (Y,)
+    return (Global,), ()
+
+
+def _vec_access_ok(km, index_kind, write):
+    core, c = split_const(km.access)
+    moving, zero = _moving(index_kind)
+    vc = vec_class(core, moving, zero)
+    if vc.kind == AFF and vc.al and c % 4 == 0:
+        return True
+    return vc.kind == INV and not write
+
+
+def _vec_operand_ok(k, index_kind):
+    if isinstance(k, KConstant):
+        return True
+    if isinstance(k, KConcat):
+        moving, zero = _moving(index_kind)
+        return (vec_class(k.condition, moving, zero).kind == INV
+                and _vec_operand_ok(k.karg_one, index_kind) and _vec_operand_ok(k.karg_two, index_kind))
+    return k.is_temp or _vec_access_ok(k, index_kind, False)
+
+
+def _vector_plan(stmts, n, index_kind="global", n_cols=1):
+    """Lane layout for 4 elements per thread: every read must be contiguous
+    and 4-aligned, or constant over aligned groups of 4 (a concat's condition
+    too), and every write contiguous and aligned, with folded offsets that
+    are multiples of 4 floats."""
+    if n % 4 != 0 or (index_kind == "dp" and n_cols % 4 != 0):
         return False
     for kind, node in stmts:
-        if kind == "sum":
-            return False
-        if kind in ("tmp", "load", "store"):
+        if kind in ("tmp", "load", "store", "sum"):
             continue
-        ks = list(node.kargs) + [node.kres]
-        for k in ks:
-            if isinstance(k, KConcat):
+        for k in node.kargs:
+            if not _vec_operand_ok(k, index_kind):
                 return False
-            if isinstance(k, KMatrix) and not k.is_temp:
-                core, c = split_const(k.access)
-                vc = vec_class(core, Global)
-                if vc.kind == AFF and vc.al and c % 4 == 0:
-                    continue
-                if vc.kind == INV and k is not node.kres:
-                    continue
-                return False
+        if not node.kres.is_temp and not _vec_access_ok(node.kres, index_kind, True):
+            return False
     return True
+
+
+def _index_setup(index_kind, ity, n_cols):
+    if index_kind == "dp":
+        return (f"const {ity} _x = _global_id / ({ity}){n_cols}; "
+                f"const {ity} _y = _global_id % ({ity}){n_cols}; (void)_x; (void)_y;")
+    if index_kind == "red":
+        return f"const {ity} _x = _global_id; const {ity} _y = 0; (void)_x; (void)_y;"
+    return ""
 
 
 def elementwise_plan(stmts, n, index_kind="global", n_cols=1, flops=0, init_value=None) -> KernelPlan:
@@ -455,14 +566,8 @@ def elementwise_plan(stmts, n, index_kind="global", n_cols=1, flops=0, init_valu
     params = Params()
     bound = _expr_bound(stmts, max(n - 1, 0), max(n - 1, 0), max(n_cols - 1, 0))
     ity = _ity(bound)
-    setup = ""
-    if index_kind == "dp":
-        setup = (f"const {ity} _x = _global_id / ({ity}){n_cols}; "
-                 f"const {ity} _y = _global_id % ({ity}){n_cols}; (void)_x; (void)_y;")
-    elif index_kind == "red":
-        setup = f"const {ity} _x = _global_id; const {ity} _y = 0; (void)_x; (void)_y;"
-    vec = index_kind == "global" and _vector_plan(stmts, n)
-    if not vec:
+    setup = _index_setup(index_kind, ity, n_cols)
+    if not _vector_plan(stmts, n, index_kind, n_cols):
         low = Lowerer(ity, params)
         body = "\n    ".join(low.statements(stmts, init_value))
         src = f"""extern "C" __global__ void __launch_bounds__({BLOCK}) {KNAME}({_params_decl(params)}{', ' if params.slots else ''}unsigned long long n_) {{
@@ -474,18 +579,18 @@ def elementwise_plan(stmts, n, index_kind="global", n_cols=1, flops=0, init_valu
 """
         grid = (max(1, ceil(n / BLOCK)), 1, 1)
     else:
-        src = _vector_source(stmts, ity, params)
+        src = _vector_source(stmts, ity, params, setup, index_kind)
         grid = (max(1, ceil(n / (4 * BLOCK))), 1, 1)
     return KernelPlan(src, grid, (BLOCK, 1, 1), _plan_args(params, (n,)), family="elw", flops=flops)
 
 
-def _vector_source(stmts, ity, params: Params) -> str:
+def _vector_source(stmts, ity, params: Params, setup="", index_kind="global") -> str:
     """Four consecutive elements per thread: float4 loads/stores for aligned
-    contiguous accesses, one scalar load for group-constant accesses."""
+    contiguous accesses, one scalar load for group-constant accesses, a
+    concat evaluated once per group (its condition is group-constant)."""
     lines = []
-    loaded: Dict[tuple, str] = {}
+    loaded: Dict[tuple, List[str]] = {}
     written: Dict[tuple, str] = {}
-    temps = []
     cnt = [0]
 
     def fresh(prefix):
@@ -494,31 +599,50 @@ def _vector_source(stmts, ity, params: Params) -> str:
 
     def loc(km):
         core, c = split_const(km.access)
-        p = params.ptr("buf", km.id, c)
+        if getattr(km, "scratch_offset", None) is not None:
+            p = params.ptr("scratch", 0, km.scratch_offset + c)
+        else:
+            p = params.ptr("buf", km.id, c)
         return p, core, (p, repr(core))
 
-    def operand(k):
+    def vec_expr(k):
+        """A float4-valued expression for an operand (lazy for concats)."""
         if isinstance(k, KConstant):
-            lit = const_literal(k.constant)
-            return [lit] * 4
+            lit = f"(float)({const_literal(k.constant)})"
+            return f"make_float4({lit}, {lit}, {lit}, {lit})"
+        if isinstance(k, KConcat):
+            cond = lower_index(k.condition, ity)
+            return f"(({cond}) ? {vec_expr(k.karg_two)} : {vec_expr(k.karg_one)})"
         if k.is_temp:
-            return [f"temp_{k.id}[{i}]" for i in range(4)]
+            return f"make_float4(temp_{k.id}[0], temp_{k.id}[1], temp_{k.id}[2], temp_{k.id}[3])"
         p, core, key = loc(k)
         if key in written:
-            return [f"{written[key]}.{c}" for c in "xyzw"]
-        if key in loaded:
-            return loaded[key]
-        vc = vec_class(core, Global)
+            return written[key]
         idx = lower_index(core, ity)
-        if vc.kind == AFF:
-            v = fresh("v")
-            lines.append(f"const float4 {v} = *reinterpret_cast<const float4*>({p} + {idx});")
-            vals = [f"{v}.{c}" for c in "xyzw"]
-        else:
-            v = fresh("s")
-            lines.append(f"const float {v} = {p}[{idx}];")
-            vals = [v] * 4
-        loaded[key] = vals
+        moving, zero = _moving(index_kind)
+        if vec_class(core, moving, zero).kind == AFF:
+            return f"(*reinterpret_cast<const float4*>({p} + {idx}))"
+        v = f"{p}[{idx}]"
+        return f"make_float4({v}, {v}, {v}, {v})"
+
+    def operand(k):
+        """Per-lane expressions of an operand; loads are hoisted into locals
+        in program order (a location read twice is loaded once)."""
+        if isinstance(k, KConstant):
+            return [const_literal(k.constant)] * 4
+        if isinstance(k, KMatrix) and k.is_temp:
+            return [f"temp_{k.id}[{i}]" for i in range(4)]
+        if isinstance(k, KMatrix):
+            p, core, key = loc(k)
+            if key in written:
+                return [f"{written[key]}.{c}" for c in "xyzw"]
+            if key in loaded:
+                return loaded[key]
+        v = fresh("v")
+        lines.append(f"const float4 {v} = {vec_expr(k)};")
+        vals = [f"{v}.{c}" for c in "xyzw"]
+        if isinstance(k, KMatrix):
+            loaded[loc(k)[2]] = vals
         return vals
 
     def rhs(kind, n, lane):
@@ -529,6 +653,8 @@ def _vector_source(stmts, ity, params: Params) -> str:
             return f"{op(n.kargs[0])} {o} {op(n.kargs[1])}"
         if kind == "copy":
             return op(n.kargs[0])
+        if kind == "init":
+            return f"_value.{'xyzw'[lane]}"
         a = op(n.kargs[0])
         u = n.op
         if u == UnaryOp.EXP2:
@@ -547,7 +673,6 @@ def _vector_source(stmts, ity, params: Params) -> str:
 
     for kind, n in stmts:
         if kind == "tmp":
-            temps.append(n.id)
             lines.append(f"float temp_{n.id}[4] = {{0.0f, 0.0f, 0.0f, 0.0f}};")
             continue
         if kind == "load":
@@ -560,6 +685,21 @@ def _vector_source(stmts, ity, params: Params) -> str:
             tid, off = n
             lines.append(f"*reinterpret_cast<float4*>({params.ptr('scratch', 0, off)} + _global_id) = "
                          f"make_float4(temp_{tid}[0], temp_{tid}[1], temp_{tid}[2], temp_{tid}[3]);")
+            continue
+        if kind == "sum":
+            off, chunks, count, op, pad_zero = n
+            pp = params.ptr("scratch", 0, off)
+            lines.append(f"float4 _value = *reinterpret_cast<const float4*>({pp} + _global_id);")
+            for c in range(1, chunks):
+                v = fresh("v")
+                lines.append(f"const float4 {v} = *reinterpret_cast<const float4*>({pp} + "
+                             f"(unsigned long long)_global_id + {c * count}ull);")
+                for lane in "xyzw":
+                    lines.append(f"_value.{lane} = fmaxf(_value.{lane}, {v}.{lane});" if op
+                                 else f"_value.{lane} = _value.{lane} + {v}.{lane};")
+            if op and pad_zero:
+                for lane in "xyzw":
+                    lines.append(f"_value.{lane} = fmaxf(_value.{lane}, 0.0f);")
             continue
         # operands are loaded before the statement computes (program order)
         for k in n.kargs:
@@ -579,6 +719,7 @@ def _vector_source(stmts, ity, params: Params) -> str:
     return f"""extern "C" __global__ void __launch_bounds__({BLOCK}) {KNAME}({_params_decl(params)}{', ' if params.slots else ''}unsigned long long n_) {{
   const {ity} _global_id = (({ity})blockIdx.x * {BLOCK}u + threadIdx.x) * 4u;
   if (_global_id >= ({ity})n_) return;
+  {setup}
   {body}
 }}
 """
@@ -651,7 +792,8 @@ def dotprod_plan(stmts, dp, A=None, B=None, config=None, partial_off=None) -> Ke
     (kernels/dotprod.py:7-43, dp_elw_fuse.py:26-65 semantics).  ``A``/``B``
     replace the node's operands (a gathered copy in scratch); with a K split
     (``config[2] > 1``) the blocks store partial products to scratch at
-    ``partial_off`` ([chunk][M][N]) and ``stmts`` must be empty."""
+    ``partial_off`` ([chunk][M][N]) and ``stmts`` must be empty; so does an
+    unsplit product whose epilogue runs as a separate pass."""
     M, N = dp.shape
     K = dp.children_shapes[0][1]
     BM, BN, split = config if config is not None else dp_config(M, N, K)
@@ -662,8 +804,8 @@ def dotprod_plan(stmts, dp, A=None, B=None, config=None, partial_off=None) -> Ke
     params = Params()
     la, _ = _loader_struct("LA", A, "A", params, ity, (M, K))
     lb, _ = _loader_struct("LB", B, "B", params, ity, (K, N))
-    if split > 1:
-        assert not stmts, "a split DotProd stores partial products only"
+    if partial_off is not None:
+        assert not stmts, "a DotProd storing partial products runs no epilogue"
         pp = params.ptr("scratch", 0, partial_off)
         body = (f"{pp}[((unsigned long long)_chunk * {M}ull + _x) * {N}ull + _y] = _value;")
     else:
@@ -760,7 +902,8 @@ def reduce_plan(stmts, red, partial_off=None) -> KernelPlan:
     ld = (f"struct LD {{ static constexpr bool kVec = {'true' if vec else 'false'}; @FIELDS@\n"
           f"  __device__ float at({ity} _x, {ity} _y) const {{ (void)_x; (void)_y; {at} }}\n"
           f"  __device__ float4 at4({ity} _x, {ity} _y) const {{ (void)_x; (void)_y; {at4} }}\n{inc_fn}}};\n")
-    if split > 1:
+    if partial_off is not None:
+        assert split > 1, "only a split Reduce stores partial results"
         assert not stmts, "a split Reduce stores partial results only"
         pp = params.ptr("scratch", 0, partial_off)
         body = f"{pp}[(unsigned long long)_chunk * {V}ull + _x] = _v;"
@@ -889,11 +1032,24 @@ def command_plans(cmd, buffers: BufferInfo, scratch_base: int):
     else:
         raise TypeError(f"Encountered unexpected cmd: {cmd}")
 
-    pairs = conflict_pairs(stmts, buffers, kind, cols)
-    if any(i == j for i, j in pairs):
-        return lockstep_plans(stmts, n, kind, cols, init, scratch_base) + (True,)
-    plans, need = phased_plans(stmts, pairs, n, kind, cols, init, scratch_base)
-    return plans, need, len(plans) > 1
+    # an elementwise command is split into independent groups, each its own
+    # kernel with its own ranges (same-shaped groups then share one launch)
+    groups = [stmts] if init is not None else components(stmts, buffers)
+    plans, end, multipass = [], scratch_base, False
+    for group in groups:
+        pairs = conflict_pairs(group, buffers, kind, cols)
+        if any(i == j for i, j in pairs):
+            ps, need = lockstep_plans(group, n, kind, cols, init, end)
+        else:
+            ps, need = phased_plans(group, pairs, n, kind, cols, init, end)
+        reads, writes = stmt_regions(group, buffers) if len(groups) > 1 else (None, None)
+        for p in ps:
+            p.reads, p.writes = reads, writes
+            p.scratch = (end - scratch_base, end - scratch_base + need)
+        plans.extend(ps)
+        multipass |= len(ps) > 1
+        end += need
+    return plans, end - scratch_base, multipass
 
 
 class ScratchAlloc:
@@ -938,6 +1094,25 @@ def _dense_scratch_operand(off, cols):
     return _scratch_km(off, Add(Mult(X(), Val(Constant(cols))), Y()))
 
 
+# a DotProd epilogue reading more distinct buffer locations than this runs as
+# its own elementwise pass over the stored product (the MFMA accumulator
+# layout makes wide epilogue loads slow and costs registers)
+EPILOGUE_MAX_LOADS = 4
+
+
+def epilogue_loads(part):
+    """Distinct non-temp operand locations an epilogue reads."""
+    seen = set()
+    for kind, n in part:
+        if kind in ("tmp", "load", "store", "sum", "init"):
+            continue
+        for k in n.kargs:
+            for km in _iter_kmatrix(k):
+                if not km.is_temp:
+                    seen.add((km.id, getattr(km, "scratch_offset", None), repr(km.access)))
+    return len(seen)
+
+
 def first_pass_plans(part, n, init_node, alloc: ScratchAlloc):
     """Plans of the pass that runs the DotProd or Reduce of a command with
     ``part`` as its epilogue: operand gathers, then the product (or the
@@ -958,7 +1133,7 @@ def first_pass_plans(part, n, init_node, alloc: ScratchAlloc):
             off = alloc.take(K * N)
             pre.append(gather_plan(B, K, N, off))
             B = _dense_scratch_operand(off, N)
-        if cfg[2] == 1:
+        if cfg[2] == 1 and epilogue_loads(part) <= EPILOGUE_MAX_LOADS:
             return pre + [dotprod_plan(part, init_node, A, B, cfg)]
         poff = alloc.take(cfg[2] * M * N)
         main = dotprod_plan([], init_node, A, B, cfg, partial_off=poff)

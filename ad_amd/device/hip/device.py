@@ -147,9 +147,6 @@ class HIPDevice(Device):
             if cursor + need > ring:
                 cursor = 0
             self._scratch_base[cmd.program_id] = cursor
-            reads, writes = regions[cmd.program_id]
-            reads.append(("scratch", cursor, cursor + need))
-            writes.append(("scratch", cursor, cursor + need))
             cursor += need
         self.scratch_off = off
         off += _align(ring * 4)
@@ -231,8 +228,15 @@ class HIPDevice(Device):
                     return
                 launches = []
                 for cmd in stretch:
-                    reads, writes = regions[cmd.program_id]
+                    c_reads, c_writes = regions[cmd.program_id]
+                    base = self._scratch_base.get(cmd.program_id, 0)
                     for plan in plans[cmd.program_id]:
+                        reads = list(c_reads if plan.reads is None else plan.reads)
+                        writes = list(c_writes if plan.writes is None else plan.writes)
+                        lo, hi = plan.scratch
+                        if hi > lo:
+                            reads.append(("scratch", base + lo, base + hi))
+                            writes.append(("scratch", base + lo, base + hi))
                         launches.append(_Launch(cmd, plan, None, reads, writes))
                 key = (lambda L: (L.plan.name, L.plan.grid, L.plan.block, L.plan.shared)) \
                     if self.group_launches else (lambda L: None)

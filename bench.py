@@ -219,6 +219,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-micro", action="store_true", help="skip the single-command benchmarks")
+    ap.add_argument("--micro-only", action="store_true",
+                    help="run only the single-command benchmarks (for counter passes)")
     ap.add_argument("--eager", action="store_true",
                     help="launch the step's kernels one by one instead of replaying a HIP graph "
                          "(for kernel-trace profilers)")
@@ -248,6 +250,9 @@ def main():
                          "gbs": round(elw["gbs"], 1), "frac": round(elw["gbs"] / PEAK_HBM_GBS, 4)},
         }
 
+    if args.micro_only:
+        print(json.dumps({"microbench": micro or None}), flush=True)
+        return
     tr = transformer_steps(args.config, args.steps, args.warmup, eager=args.eager)
     value = args.steps / tr["wall_s"]
     ms_per_step = tr["wall_s"] * 1e3 / args.steps

@@ -156,3 +156,135 @@ def test_generated_kernels_compile_for_gfx950():
     for c in cmds:
         for plan in codegen.command_plans(c, info, 0)[0]:
             assert len(compile_source(header + plan.source)) > 0
+
+
+# ---------------------------------------------------------------- components
+class _Stmt:
+    def __init__(self, kargs, kres):
+        self.kargs, self.kres = kargs, kres
+
+
+class _Decl:
+    def __init__(self, i):
+        self.id = i
+
+
+def _km(i, temp=False, var=None):
+    from ad_amd.expr import Global
+    from ad_amd.kernalize import KMatrix
+    k = KMatrix(i, Global(), [1])
+    k.is_temp = temp
+    if var is not None:
+        k.tetris_var = var
+    return k
+
+
+@pytest.mark.parametrize("seed", range(60))
+def test_components_keep_linked_statements_together(seed):
+    """Statements sharing a temp, or touching overlapping ranges with at
+    least one write, end up in one group; groups keep statement order."""
+    import random
+    from ad_amd.device.hip import codegen
+    rng = random.Random(seed)
+    info = codegen.BufferInfo()
+    info.size = {1: 100, 2: 100}
+    stmts, temps = [], []
+    for i in range(rng.randint(1, 30)):
+        def opnd():
+            if rng.random() < 0.3 and temps:
+                return _km(rng.choice(temps), temp=True)
+            return _km(rng.choice([1, 1, 2]), var=(rng.randint(0, 99), rng.randint(0, 90), rng.randint(1, 10)))
+        kargs = [opnd() for _ in range(rng.randint(1, 2))]
+        if rng.random() < 0.4:
+            t = 1000 + i
+            temps.append(t)
+            stmts.append(("tmp", _Decl(t)))
+            kres = _km(t, temp=True)
+        else:
+            kres = _km(rng.choice([1, 2]), var=(rng.randint(0, 99), rng.randint(0, 90), rng.randint(1, 10)))
+        stmts.append(("bin", _Stmt(kargs, kres)))
+    groups = codegen.components(stmts, info)
+    gid = {id(st): g for g, grp in enumerate(groups) for st in grp}
+    assert len(gid) == len(stmts)
+
+    def acc(st):
+        kind, n = st
+        if kind == "tmp":
+            return [], [], {n.id}
+        rs, ws, ts = [], [], set()
+        for a in n.kargs:
+            (ts.add(a.id) if a.is_temp else rs.append(codegen._region(a, info)[0]))
+        (ts.add(n.kres.id) if n.kres.is_temp else ws.append(codegen._region(n.kres, info)[0]))
+        return rs, ws, ts
+
+    def ov(p, q):
+        return p[0] == q[0] and max(p[1], q[1]) < min(p[2], q[2])
+    for a in stmts:
+        for b in stmts:
+            if a is b:
+                continue
+            ra, wa, ta = acc(a)
+            rb, wb, tb = acc(b)
+            if (ta & tb) or any(ov(x, y) for x in wa for y in rb + wb) or any(ov(x, y) for x in wb for y in ra):
+                assert gid[id(a)] == gid[id(b)]
+    pos = {id(st): i for i, st in enumerate(stmts)}
+    for grp in groups:
+        idx = [pos[id(st)] for st in grp]
+        assert idx == sorted(idx)
+
+
+@settings(max_examples=300, deadline=None)
+@given(exprs(depth=3, leaves=(Global, X, Y)))
+def test_vec_class_two_moving_variables_is_sound(e):
+    """In a DotProd element space with rows of 64 (g = 64x + y), X is
+    constant and Global, Y advance inside aligned groups of 4: AFF means
+    f(4t+i) = f(4t) + i and INV means f(4t+i) = f(4t)."""
+    vc = analysis.vec_class(e, (Global, Y))
+    for x in (0, 1, 5):
+        for t in range(0, 64, 4):
+            base = evaluate(e, g=64 * x + t, x=x, y=t)
+            for i in range(4):
+                v = evaluate(e, g=64 * x + t + i, x=x, y=t + i)
+                if vc.kind == analysis.AFF:
+                    assert v == base + i
+                elif vc.kind == analysis.INV:
+                    assert v == base
+            if vc.kind == analysis.AFF and vc.al:
+                assert base % 4 == 0
+
+
+def test_combine_passes_follow_a_partial_store():
+    """Every elementwise pass that combines stored products or partial
+    reductions comes right after the pass that stores them, into the same
+    scratch location (a missing store would leave the combine reading stale
+    scratch)."""
+    import ad_amd as ad
+    from ad_amd import workloads
+    from ad_amd.alloc import AllocEntry
+    from ad_amd.graph import ForNode
+    ad.reset()
+    workloads.transformer(layers=1, d_model=64, heads=4, ff=64, seq=8, batch=2, steps=1, receive=False)
+    proc = ad.compile_proc()
+    info = codegen.BufferInfo()
+
+    def note(c, _):
+        if isinstance(c, AllocEntry):
+            info.size[c.id] = c.size
+        return c
+    proc.walk(note, step_fused=False, step_proc=True)
+    inner = [c for c in proc.procedure if isinstance(c, ForNode)][0].get_proc()
+    combines = 0
+    for cmd in inner.procedure:
+        if type(cmd).__name__ in ("Feeder", "Receiver", "AllocEntry", "DeallocEntry"):
+            continue
+        plans, _, _ = codegen.command_plans(cmd, info, 0)
+        for i, p in enumerate(plans):
+            if "_value = *reinterpret_cast<const float4*>" in p.source or "float _value = p" in p.source:
+                combines += 1
+                prev = plans[i - 1]
+                assert prev.family in ("dotprod", "reduce")
+                assert re.search(r"\] = _v(alue)?;", prev.source), prev.source[-600:]
+                slot = [a for a in p.args if a[0] == "scratch"]
+                assert any(a in prev.args for a in slot)
+    assert combines > 0
+    ad.reset()
