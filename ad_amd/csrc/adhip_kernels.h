@@ -31,9 +31,10 @@ __device__ __forceinline__ float rop(float a, float b) {
 // LA::kMode: 0 = contiguous along k, 1 = contiguous along m.
 // LB::kMode: 0 = contiguous along n, 1 = contiguous along k.
 //
-// Block tile BM x BN, K panels of DP_BK staged in LDS, 4 waves as 2 x 2, each
-// wave (BM/2) x (BN/2) made of 32x32 v_mfma_f32_32x32x2f32 tiles; the next
-// panel is prefetched into registers while the current one is consumed.
+// Block tile BM x BN, K panels of DP_BK staged in two LDS buffers, 4 waves as
+// 2 x 2, each wave (BM/2) x (BN/2) made of 32x32 v_mfma_f32_32x32x2f32 tiles;
+// the next panel is prefetched into registers while the current one is
+// consumed, then stored into the other buffer.
 // SPLIT > 1 splits K into SPLIT chunks: blockIdx.y = tile row + tiles_m *
 // chunk, and the epilogue receives the chunk index (partial results).
 // The epilogue is called as epi(value, row, col, chunk) in registers.
@@ -46,8 +47,8 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
   constexpr int VA = BM * DP_BK / 4 / 256;               // float4 loads per thread
   constexpr int VB = BN * DP_BK / 4 / 256;
   static_assert(VA >= 1 && VB >= 1, "tile too small for 256 threads");
-  __shared__ float As[DP_BK][BM + DP_PAD];
-  __shared__ float Bs[DP_BK][BN + DP_PAD];
+  __shared__ float As[2][DP_BK][BM + DP_PAD];
+  __shared__ float Bs[2][DP_BK][BN + DP_PAD];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -103,17 +104,17 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
       }
     }
   };
-  auto store_a = [&]() {
+  auto store_a = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < VA; ++i) {
       const int v = tid + 256 * i;
       if constexpr (LA::kMode == 0) {
         const int m = v / (DP_BK / 4), k = 4 * (v % (DP_BK / 4));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) As[k + j][m] = ra[i][j];
+        for (int j = 0; j < 4; ++j) As[buf][k + j][m] = ra[i][j];
       } else {
         const int k = v / (BM / 4), m = 4 * (v % (BM / 4));
-        *reinterpret_cast<float4*>(&As[k][m]) = make_float4(ra[i][0], ra[i][1], ra[i][2], ra[i][3]);
+        *reinterpret_cast<float4*>(&As[buf][k][m]) = make_float4(ra[i][0], ra[i][1], ra[i][2], ra[i][3]);
       }
     }
   };
@@ -142,17 +143,17 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
       }
     }
   };
-  auto store_b = [&]() {
+  auto store_b = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < VB; ++i) {
       const int v = tid + 256 * i;
       if constexpr (LB::kMode == 0) {
         const int k = v / (BN / 4), n = 4 * (v % (BN / 4));
-        *reinterpret_cast<float4*>(&Bs[k][n]) = make_float4(rb[i][0], rb[i][1], rb[i][2], rb[i][3]);
+        *reinterpret_cast<float4*>(&Bs[buf][k][n]) = make_float4(rb[i][0], rb[i][1], rb[i][2], rb[i][3]);
       } else {
         const int n = v / (DP_BK / 4), k = 4 * (v % (DP_BK / 4));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) Bs[k + j][n] = rb[i][j];
+        for (int j = 0; j < 4; ++j) Bs[buf][k + j][n] = rb[i][j];
       }
     }
   };
@@ -165,13 +166,17 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
+  // Two LDS buffers: the panel prefetched into registers during the
+  // products of the current panel is stored into the other buffer, so one
+  // barrier per panel separates every write of a buffer from its last read.
   const int lk = lane >> 5, lr = lane & 31;
   if (kbeg < kend) {
     load_a(kbeg);
     load_b(kbeg);
-    store_a();
-    store_b();
+    store_a(0);
+    store_b(0);
     __syncthreads();
+    int cur = 0;
     for (int k0 = kbeg; k0 < kend; k0 += DP_BK) {
       const bool more = k0 + DP_BK < kend;
       if (more) {
@@ -182,21 +187,21 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
       for (int kk = 0; kk < DP_BK; kk += 2) {
         float a[TM], b[TN];
 #pragma unroll
-        for (int i = 0; i < TM; ++i) a[i] = As[kk + lk][wm * (BM / 2) + i * 32 + lr];
+        for (int i = 0; i < TM; ++i) a[i] = As[cur][kk + lk][wm * (BM / 2) + i * 32 + lr];
 #pragma unroll
-        for (int j = 0; j < TN; ++j) b[j] = Bs[kk + lk][wn * (BN / 2) + j * 32 + lr];
+        for (int j = 0; j < TN; ++j) b[j] = Bs[cur][kk + lk][wn * (BN / 2) + j * 32 + lr];
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
           for (int j = 0; j < TN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
       }
-      __syncthreads();
       if (more) {
-        store_a();
-        store_b();
-        __syncthreads();
+        store_a(cur ^ 1);
+        store_b(cur ^ 1);
       }
+      __syncthreads();
+      cur ^= 1;
     }
   }
   // 32x32 accumulator layout: lane holds column (lane % 32) and rows

@@ -35,6 +35,16 @@ from .analysis import AFF, INV, const_of, split_const, upper_bound, vec_class
 
 BLOCK = 256
 _TEMP_RE = re.compile(r"\btemp_\d+\b")
+_HEADER = []
+
+
+def _header_text() -> str:
+    """Text of the device template header every kernel is compiled with."""
+    if not _HEADER:
+        from .runtime import HEADER_PATH
+        with open(HEADER_PATH) as fh:
+            _HEADER.append(fh.read())
+    return _HEADER[0]
 
 _OPS = {Add: "+", Minus: "-", Mult: "*", Div: "/", Remainder: "%", ShiftRight: ">>",
         ShiftLeft: "<<", BitwiseAnd: "&", MoreThan: ">", LessThan: "<"}
@@ -66,7 +76,9 @@ class KernelPlan:
         # own symbol so profiles tell kernels apart
         tag = {"dotprod": "dp", "reduce": "red", "elw": "elw", "copy": "copy"}.get(self.family, "k")
         self.source = _table_entry(self.source, len(self.args))
-        self.name = f"adhip_{tag}_{hashlib.sha1(self.source.encode()).hexdigest()[:12]}"
+        # the symbol hashes the template header too, so a changed template
+        # gives new symbols (profiles name the kernel that was measured)
+        self.name = f"adhip_{tag}_{hashlib.sha1((_header_text() + self.source).encode()).hexdigest()[:12]}"
         self.source = self.source.replace(KNAME, self.name)
 
     @property

@@ -181,6 +181,7 @@ def transformer(layers=1, d_model=32, heads=4, ff=64, seq=4, batch=1, steps=2, l
     net = [BatchedEncoderLayer(d_model, heads, ff, batch, seq) for _ in range(layers)]
     params = [p for layer in net for p in layer.parameters()]
     set_uniform(params, 0)
+    tensors = list(params)            # SGD.step replaces the entries of ``params``
     opt = SGD(params, lr=lr)
     rows = batch * seq
     x = np.random.default_rng(1).standard_normal((rows, d_model), dtype=np.float32)
@@ -194,7 +195,7 @@ def transformer(layers=1, d_model=32, heads=4, ff=64, seq=4, batch=1, steps=2, l
         (out * out * (1.0 / (rows * d_model))).backward()
         opt.step()
     ir_for(range(steps), body)
-    res = {"params_ref": params}
+    res = {"params_ref": tensors, "net": net, "x": x}
     if receive:
         Receiver(lambda *a: res.setdefault("params", [v.copy() for v in a]), opt.parameters)
     return res

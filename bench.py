@@ -42,6 +42,21 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def measured_traffic(kernel):
+    """HBM bytes per dispatch of ``kernel`` from the committed counter
+    summary (two rocprofv3 --pmc passes, calibrated on the ElwFuse kernel),
+    or None when that summary was taken of another build of the kernel."""
+    path = os.path.join(ROOT, "profiles", "micro_hbm_traffic_counters.txt")
+    if not os.path.exists(path):
+        return None
+    with open(path) as fh:
+        for line in fh:
+            parts = line.split()
+            if len(parts) == 3 and parts[0] == "traffic" and parts[1] == kernel:
+                return int(parts[2])
+    return None
+
+
 def _commands(proc):
     from ad_amd.fusion import FuseBase
     from ad_amd.node import Node
@@ -270,7 +285,7 @@ def main():
     if micro:
         dp = micro["dotprod_elw"]
         roofline = {"bound": "mfma", "achieved": dp["tflops"], "peak": PEAK_FP32_MFMA_TFLOPS,
-                    "unit": "TFLOP/s", "frac": dp["frac"], "traffic": None,
+                    "unit": "TFLOP/s", "frac": dp["frac"], "traffic": measured_traffic(dp["kernel"]),
                     "kernel": dp["kernel"],
                     "workload": "DotProd+Elw sigmoid(A@B+bias), [4096,4096]x[4096,4096] fp32, "
                                 "2*4096^3 flop per launch"}
