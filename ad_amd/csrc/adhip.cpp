@@ -19,6 +19,7 @@ namespace {
 constexpr size_t kStageSlotBytes = 8u << 20;   // pinned staging: 8 slots x 8 MiB
 constexpr int kStageSlots = 8;
 constexpr int kEventSlots = 64;
+constexpr int kTags = 4;                        // transfer-stream staging sets
 
 thread_local std::string g_tls_error;
 
@@ -44,6 +45,15 @@ struct adhip_ctx {
   int stage_next = 0;
   bool capturing = false;
   hipEvent_t events[kEventSlots] = {};
+  // transfer stream for staged host->device copies overlapped with compute
+  hipStream_t xfer = nullptr;
+  struct Tag {
+    char* host = nullptr;          // pinned staging of this set
+    size_t cap = 0, used = 0;
+    hipEvent_t copied = nullptr;   // on xfer: the set's copies are done
+    hipEvent_t released = nullptr; // on stream: the set's device data is consumed
+    bool copied_pending = false, released_pending = false, open = false;
+  } tags[kTags];
   std::vector<adhip_module*> modules;
   std::string err;
 };
@@ -119,6 +129,13 @@ void adhip_destroy(adhip_ctx* ctx) {
   for (int i = 0; i < kStageSlots; ++i)
     if (ctx->stage_done[i]) hipEventDestroy(ctx->stage_done[i]);
   if (ctx->stage) hipHostFree(ctx->stage);
+  if (ctx->xfer) hipStreamSynchronize(ctx->xfer);
+  for (auto& t : ctx->tags) {
+    if (t.copied) hipEventDestroy(t.copied);
+    if (t.released) hipEventDestroy(t.released);
+    if (t.host) hipHostFree(t.host);
+  }
+  if (ctx->xfer) hipStreamDestroy(ctx->xfer);
   if (ctx->arena) hipFree(ctx->arena);
   if (ctx->stream) hipStreamDestroy(ctx->stream);
   delete ctx;
@@ -145,6 +162,7 @@ int adhip_arena_reserve(adhip_ctx* ctx, size_t bytes, uint64_t* dev_base) {
   HIP_TRY(ctx, hipSetDevice(ctx->device));
   if (ctx->arena) {
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    if (ctx->xfer) HIP_TRY(ctx, hipStreamSynchronize(ctx->xfer));
     HIP_TRY(ctx, hipFree(ctx->arena));
     ctx->arena = nullptr;
     ctx->arena_bytes = 0;
@@ -177,6 +195,71 @@ int adhip_write(adhip_ctx* ctx, uint64_t dst_off, const void* host, size_t bytes
     ctx->stage_used[slot] = true;
     done += n;
   }
+  return 0;
+}
+
+int adhip_stage_begin(adhip_ctx* ctx, int tag) {
+  if (!ctx || tag < 0 || tag >= kTags) return fail(ctx, ADHIP_E_ARG, "bad staging set %d", tag);
+  if (ctx->capturing) return fail(ctx, ADHIP_E_STATE, "staged copies during graph capture");
+  auto& t = ctx->tags[tag];
+  if (t.open) return fail(ctx, ADHIP_E_STATE, "staging set %d already open", tag);
+  HIP_TRY(ctx, hipSetDevice(ctx->device));
+  if (!ctx->xfer) HIP_TRY(ctx, hipStreamCreateWithFlags(&ctx->xfer, hipStreamNonBlocking));
+  if (!t.copied) HIP_TRY(ctx, hipEventCreateWithFlags(&t.copied, hipEventDisableTiming));
+  if (!t.released) HIP_TRY(ctx, hipEventCreateWithFlags(&t.released, hipEventDisableTiming));
+  // the pinned buffer is reused: its previous copies must have left it
+  if (t.copied_pending) HIP_TRY(ctx, hipEventSynchronize(t.copied));
+  t.copied_pending = false;
+  // the device data of this set is rewritten: its previous readers must be done
+  if (t.released_pending) HIP_TRY(ctx, hipStreamWaitEvent(ctx->xfer, t.released, 0));
+  t.used = 0;
+  t.open = true;
+  return 0;
+}
+
+int adhip_stage_write(adhip_ctx* ctx, int tag, uint64_t dst_off, const void* host, size_t bytes) {
+  if (!ctx || tag < 0 || tag >= kTags || (!host && bytes)) return fail(ctx, ADHIP_E_ARG, "bad argument");
+  auto& t = ctx->tags[tag];
+  if (!t.open) return fail(ctx, ADHIP_E_STATE, "staging set %d not open", tag);
+  if (int r = check_range(ctx, dst_off, bytes)) return r;
+  const size_t need = t.used + ((bytes + 255) & ~size_t(255));
+  if (need > t.cap) {
+    // nothing of this set is in flight (stage_begin waited), so it may move
+    char* bigger = nullptr;
+    const size_t cap = need > 2 * t.cap ? need : 2 * t.cap;
+    HIP_TRY(ctx, hipHostMalloc((void**)&bigger, cap, hipHostMallocDefault));
+    if (t.host) {
+      HIP_TRY(ctx, hipStreamSynchronize(ctx->xfer));   // copies of this round read the old buffer
+      std::memcpy(bigger, t.host, t.used);
+      hipHostFree(t.host);
+    }
+    t.host = bigger;
+    t.cap = cap;
+  }
+  char* staged = t.host + t.used;
+  std::memcpy(staged, host, bytes);
+  HIP_TRY(ctx, hipMemcpyAsync(ctx->arena + dst_off, staged, bytes, hipMemcpyHostToDevice, ctx->xfer));
+  t.used = need;
+  return 0;
+}
+
+int adhip_stage_end(adhip_ctx* ctx, int tag) {
+  if (!ctx || tag < 0 || tag >= kTags) return fail(ctx, ADHIP_E_ARG, "bad staging set %d", tag);
+  auto& t = ctx->tags[tag];
+  if (!t.open) return fail(ctx, ADHIP_E_STATE, "staging set %d not open", tag);
+  HIP_TRY(ctx, hipEventRecord(t.copied, ctx->xfer));
+  HIP_TRY(ctx, hipStreamWaitEvent(ctx->stream, t.copied, 0));
+  t.copied_pending = true;
+  t.open = false;
+  return 0;
+}
+
+int adhip_stage_release(adhip_ctx* ctx, int tag) {
+  if (!ctx || tag < 0 || tag >= kTags) return fail(ctx, ADHIP_E_ARG, "bad staging set %d", tag);
+  auto& t = ctx->tags[tag];
+  if (!t.released) return fail(ctx, ADHIP_E_STATE, "staging set %d never used", tag);
+  HIP_TRY(ctx, hipEventRecord(t.released, ctx->stream));
+  t.released_pending = true;
   return 0;
 }
 
@@ -338,6 +421,7 @@ void adhip_graph_destroy(adhip_graph* g) {
 int adhip_sync(adhip_ctx* ctx) {
   if (!ctx) return fail(ctx, ADHIP_E_ARG, "null ctx");
   HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  if (ctx->xfer) HIP_TRY(ctx, hipStreamSynchronize(ctx->xfer));
   return 0;
 }
 

@@ -7,8 +7,8 @@
 //                    block tile (64..256), 4 waves, LDS-staged K panels with a
 //                    register prefetch of the next panel, optional split of K
 //                    into chunks, epilogue in registers.
-//  * reduce_rows  -- Reduce+Elw, rows contiguous: one wave per row, float4 or
-//                    scalar coalesced loads, butterfly over the wave.
+//  * reduce_rows  -- Reduce+Elw, rows contiguous: waves striding over rows,
+//                    float4 or scalar coalesced loads, butterfly over the wave.
 //  * reduce_cols  -- Reduce+Elw, columns contiguous: 64 columns x 4 row groups
 //                    per block, coalesced along the columns, LDS combine,
 //                    optional split of the rows into chunks.
@@ -222,42 +222,45 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
 // LD::at(x, y) loads element y of reduced row x; LD::at4 four consecutive y.
 // LD::inc(y) is false for elements the reference's work-group tree drops.
 //
-// reduce_rows: one wave per row, four independent float4 streams per lane
-// (16 floats in flight), butterfly over the wave; lane 0 runs the epilogue.
+// reduce_rows: waves stride over the rows (a bounded grid keeps every wave
+// busy across several rows); per row, each lane keeps up to eight float4
+// loads in flight, then a butterfly over the wave; lane 0 runs the epilogue.
 template <int OP, class LD, class EPI>
 __device__ __forceinline__ void reduce_rows(const LD& ld, const EPI& epi, unsigned V, unsigned R,
                                             bool pad_zero) {
   const unsigned lane = threadIdx.x & 63;
-  const unsigned row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (row >= V) return;
+  const unsigned waves = gridDim.x * (blockDim.x >> 6);
   const float id = OP == 0 ? 0.f : -__builtin_huge_valf();
-  float acc = id;
-  if constexpr (LD::kVec) {
-    float a0 = id, a1 = id, a2 = id, a3 = id;
-    unsigned y = lane * 4;
-    for (; y + 768 < R; y += 1024) {
-      const float4 v0 = ld.at4(row, y);
-      const float4 v1 = ld.at4(row, y + 256);
-      const float4 v2 = ld.at4(row, y + 512);
-      const float4 v3 = ld.at4(row, y + 768);
-      a0 = rop<OP>(rop<OP>(rop<OP>(rop<OP>(a0, v0.x), v0.y), v0.z), v0.w);
-      a1 = rop<OP>(rop<OP>(rop<OP>(rop<OP>(a1, v1.x), v1.y), v1.z), v1.w);
-      a2 = rop<OP>(rop<OP>(rop<OP>(rop<OP>(a2, v2.x), v2.y), v2.z), v2.w);
-      a3 = rop<OP>(rop<OP>(rop<OP>(rop<OP>(a3, v3.x), v3.y), v3.z), v3.w);
-    }
-    for (; y < R; y += 256) {
-      const float4 v0 = ld.at4(row, y);
-      a0 = rop<OP>(rop<OP>(rop<OP>(rop<OP>(a0, v0.x), v0.y), v0.z), v0.w);
-    }
-    acc = rop<OP>(rop<OP>(a0, a1), rop<OP>(a2, a3));
-  } else {
-    for (unsigned y = lane; y < R; y += 64)
-      if (ld.inc(y)) acc = rop<OP>(acc, ld.at(row, y));
-  }
+  for (unsigned row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); row < V; row += waves) {
+    float acc = id;
+    if constexpr (LD::kVec) {
+      float a[8];
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) acc = rop<OP>(acc, __shfl_xor(acc, off, 64));
-  if (OP == 1 && pad_zero) acc = fmaxf(acc, 0.f);
-  if (lane == 0) epi(acc, row, 0);
+      for (int u = 0; u < 8; ++u) a[u] = id;
+      unsigned y = lane * 4;
+      for (; y + 7 * 256 < R; y += 8 * 256) {
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = ld.at4(row, y + u * 256);
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          a[u] = rop<OP>(rop<OP>(rop<OP>(rop<OP>(a[u], v[u].x), v[u].y), v[u].z), v[u].w);
+      }
+      for (; y < R; y += 256) {
+        const float4 v0 = ld.at4(row, y);
+        a[0] = rop<OP>(rop<OP>(rop<OP>(rop<OP>(a[0], v0.x), v0.y), v0.z), v0.w);
+      }
+      acc = rop<OP>(rop<OP>(rop<OP>(a[0], a[1]), rop<OP>(a[2], a[3])),
+                    rop<OP>(rop<OP>(a[4], a[5]), rop<OP>(a[6], a[7])));
+    } else {
+      for (unsigned y = lane; y < R; y += 64)
+        if (ld.inc(y)) acc = rop<OP>(acc, ld.at(row, y));
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc = rop<OP>(acc, __shfl_xor(acc, off, 64));
+    if (OP == 1 && pad_zero) acc = fmaxf(acc, 0.f);
+    if (lane == 0) epi(acc, row, 0);
+  }
 }
 
 // reduce_cols: 64 columns x 4 row groups per block, coalesced along the

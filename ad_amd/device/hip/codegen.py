@@ -789,12 +789,17 @@ def _init_list(params: Params) -> str:
 def dp_config(M, N, K):
     """Block tile and K split of a DotProd: 64-wide tiles on a narrow side,
     128 otherwise; K is split (up to 16 chunks of at least 256) while the
-    tiles alone would not give one block per compute unit."""
+    tiles alone would not give one block per compute unit, and a long K
+    (chunks of at least 1024) is split once more until two blocks share
+    each compute unit (one block's barriers then hide behind the other's
+    products)."""
     BM = 64 if M <= 64 else 128
     BN = 64 if N <= 64 else 128
     tiles = ceil(M / BM) * ceil(N / BN)
     split = 1
     while tiles * split < 256 and split < 16 and K // (2 * split) >= 256:
+        split *= 2
+    while tiles * split < 512 and split < 16 and K // (2 * split) >= 1024:
         split *= 2
     return BM, BN, split
 
@@ -932,7 +937,9 @@ def reduce_plan(stmts, red, partial_off=None) -> KernelPlan:
     src = ((ld + epi).replace("@FIELDS@", _fields(params)) +
            f"extern \"C\" __global__ void __launch_bounds__(256) {KNAME}({_params_decl(params)}) {{\n"
            f"  {call}(LD{{{init}}}, EPI{{{init}}}, {V}u, {R}u, {'true' if pad_zero else 'false'});\n}}\n")
-    grid = (ceil(V / 4), 1, 1) if mode == "rows" else (ceil(V / 64), split, 1)
+    # rows: 4 waves per block, at most 2048 blocks (8 per compute unit); the
+    # waves stride over the remaining rows
+    grid = (min(ceil(V / 4), 2048), 1, 1) if mode == "rows" else (ceil(V / 64), split, 1)
     return KernelPlan(src, grid, (256, 1, 1), _plan_args(params), family="reduce",
                       bytes=4 * V * R + 4 * V)
 

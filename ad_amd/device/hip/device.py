@@ -15,8 +15,9 @@ replays loop bodies, ``execute`` runs both passes.  Differences by design:
   (``schedule``): launches ordered by their memory conflicts, and
   independent launches of one kernel merged into one launch;
 * a loop body without Receivers is captured once as a HIP graph and the
-  graph is replayed ``len(r)`` times; a Feeder inside it copies from its own
-  staging slot, refilled from the host before each replay;
+  graph is replayed ``len(r)`` times; a Feeder inside it copies from one of
+  two staging slots, which the host refills on a transfer stream while the
+  previous iteration computes (two graphs, one per slot);
 * a Feeder writes at its arena offset (the reference OpenCL backend writes
   at offset 0, cl_helper.py:316,326 -- see ``oracle``);
 * after the run, every Tensor's host array is refreshed from the device, as
@@ -78,7 +79,9 @@ class HIPDevice(Device):
         self._contents = {}
         self._pending = []
         self._feeder_slots = {}      # feeder id -> staging byte offset
-        self._graphs = {}            # ForNode id -> (graph handle, feeders)
+        self._graphs = {}            # ForNode id -> ([graph per staging slot], feeders)
+        self._iteration = {}         # ForNode id -> iterations replayed so far
+        self._parity = 0
         self._schedules = {}         # Proc id -> [("launch", fn) | ("cmd", cmd)]
         self._capturing = False
         self.stats = {"kernels": 0, "unique_sources": 0, "multipass_cmds": 0, "launches_per_iter": 0}
@@ -123,9 +126,12 @@ class HIPDevice(Device):
 
     def _finish_init(self, proc):
         off, info = self._layout()
+        # two staging slots per Feeder: a replayed loop fills one while the
+        # graph of the previous iteration reads the other
         for fid in list(self._feeder_slots):
-            self._feeder_slots[fid] = off
-            off += _align(self._feeder_size.get(fid, 0) * 4)
+            size = _align(self._feeder_size.get(fid, 0) * 4)
+            self._feeder_slots[fid] = (off, off + size)
+            off += 2 * size
         # kernel plans and the ranges each command touches; commands that need
         # scratch get consecutive slots of a ring, so neighbouring commands do
         # not share scratch and can run in one launch
@@ -293,7 +299,7 @@ class HIPDevice(Device):
             if self._capturing:
                 # inside a graph: copy this iteration's data from the staging slot
                 dst = self.buffers[cmd.kres.id] + 4 * cmd.kres.offset
-                self.ctx.copy(dst, self._feeder_slots[cmd.id], 4 * prod(cmd.shape))
+                self.ctx.copy(dst, self._feeder_slots[cmd.id][self._parity], 4 * prod(cmd.shape))
                 self._graph_feeders.append(cmd)
                 return
             arr = self._feeder_value(cmd)
@@ -338,20 +344,35 @@ class HIPDevice(Device):
                 self._run_scheduled(inner)
             return
         if cmd.id not in self._graphs:
-            self._capturing = True
-            self._graph_feeders = []
-            self.ctx.graph_begin()
-            try:
-                self._run_scheduled(inner)
-            finally:
-                self._capturing = False
-                g = self.ctx.graph_end()
-            self._graphs[cmd.id] = (g, self._graph_feeders)
-        g, feeders = self._graphs[cmd.id]
+            graphs = []
+            for parity in (0, 1):            # one graph per staging slot
+                self._capturing, self._parity = True, parity
+                self._graph_feeders = []
+                self.ctx.graph_begin()
+                try:
+                    self._run_scheduled(inner)
+                finally:
+                    self._capturing = False
+                    graphs.append(self.ctx.graph_end())
+                if not self._graph_feeders:
+                    break                    # no Feeder: one graph serves every iteration
+            self._graphs[cmd.id] = (graphs, self._graph_feeders)
+            self._iteration[cmd.id] = 0
+        graphs, feeders = self._graphs[cmd.id]
         for _ in range(reps):
-            for f in feeders:
-                self.ctx.write(self._feeder_slots[f.id], self._feeder_value(f))
-            self.ctx.graph_launch(g)
+            if feeders:
+                # this iteration's inputs go up on the transfer stream while the
+                # previous iteration computes; the graph waits for them
+                parity = self._iteration[cmd.id] & 1
+                self.ctx.stage_begin(parity)
+                for f in feeders:
+                    self.ctx.stage_write(parity, self._feeder_slots[f.id][parity], self._feeder_value(f))
+                self.ctx.stage_end(parity)
+                self.ctx.graph_launch(graphs[parity])
+                self.ctx.stage_release(parity)
+            else:
+                self.ctx.graph_launch(graphs[0])
+            self._iteration[cmd.id] += 1
 
     def _run_proc(self, proc, func, init=False):
         """The reference's command walk (device.py:114-124), used for the init
@@ -412,8 +433,9 @@ class HIPDevice(Device):
             content.reshape(-1)[:] = out
 
     def close(self):
-        for g, _ in self._graphs.values():
-            self.ctx.graph_destroy(g)
+        for graphs, _ in self._graphs.values():
+            for g in graphs:
+                self.ctx.graph_destroy(g)
         self._graphs = {}
         self.ctx.close()
 

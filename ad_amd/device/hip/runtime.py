@@ -17,7 +17,8 @@ _lock = threading.Lock()
 
 EXPORTS = [
     "adhip_create", "adhip_destroy", "adhip_last_error", "adhip_device_info", "adhip_arena_reserve",
-    "adhip_write", "adhip_read", "adhip_copy", "adhip_compile", "adhip_free", "adhip_module_load",
+    "adhip_write", "adhip_stage_begin", "adhip_stage_write", "adhip_stage_end", "adhip_stage_release",
+    "adhip_read", "adhip_copy", "adhip_compile", "adhip_free", "adhip_module_load",
     "adhip_module_function", "adhip_launch", "adhip_graph_begin", "adhip_graph_end",
     "adhip_graph_launch", "adhip_graph_destroy", "adhip_sync", "adhip_event_record",
     "adhip_event_elapsed",
@@ -46,6 +47,10 @@ def load_library(path=LIB_PATH):
             "adhip_device_info": (i32, [vp, c.POINTER(i32), c.c_char_p, sz]),
             "adhip_arena_reserve": (i32, [vp, sz, c.POINTER(u64)]),
             "adhip_write": (i32, [vp, u64, vp, sz]),
+            "adhip_stage_begin": (i32, [vp, i32]),
+            "adhip_stage_write": (i32, [vp, i32, u64, vp, sz]),
+            "adhip_stage_end": (i32, [vp, i32]),
+            "adhip_stage_release": (i32, [vp, i32]),
             "adhip_read": (i32, [vp, u64, vp, sz]),
             "adhip_copy": (i32, [vp, u64, u64, sz]),
             "adhip_compile": (i32, [c.c_char_p, c.c_char_p, c.POINTER(vp), c.POINTER(sz), c.c_char_p, sz]),
@@ -127,6 +132,19 @@ class Context:
 
     def write(self, byte_off: int, arr):
         self.check(self.lib.adhip_write(self.h, byte_off, arr.ctypes.data, arr.nbytes), "adhip_write")
+
+    def stage_begin(self, tag: int):
+        self.check(self.lib.adhip_stage_begin(self.h, tag), "adhip_stage_begin")
+
+    def stage_write(self, tag: int, byte_off: int, arr):
+        self.check(self.lib.adhip_stage_write(self.h, tag, byte_off, arr.ctypes.data, arr.nbytes),
+                   "adhip_stage_write")
+
+    def stage_end(self, tag: int):
+        self.check(self.lib.adhip_stage_end(self.h, tag), "adhip_stage_end")
+
+    def stage_release(self, tag: int):
+        self.check(self.lib.adhip_stage_release(self.h, tag), "adhip_stage_release")
 
     def read(self, byte_off: int, arr):
         self.check(self.lib.adhip_read(self.h, byte_off, arr.ctypes.data, arr.nbytes), "adhip_read")

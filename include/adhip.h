@@ -58,6 +58,21 @@ int  adhip_write(adhip_ctx* ctx, uint64_t dst_off, const void* host, size_t byte
 /* Blocking device -> host copy after all queued work.  Replaces
  * clEnqueueReadBuffer with blocking_read (cl_helper.py:262-302). */
 int  adhip_read(adhip_ctx* ctx, uint64_t src_off, void* host, size_t bytes);
+/* Staged host -> device copies on a transfer stream, overlapped with the
+ * compute stream.  A staging set (tag 0..3) is opened, filled with copies
+ * (each host buffer is copied to pinned memory before the call returns),
+ * then closed: the compute stream waits for the set's copies before its
+ * next work.  stage_release marks, on the compute stream, the point after
+ * which the set's device data may be overwritten by the set's next round;
+ * stage_begin makes the transfer stream wait for it.  This is how a Feeder
+ * inside a replayed loop writes the next iteration's data while the current
+ * one computes.  Replaces clEnqueueWriteBuffer (cl_helper.py:304-332) for
+ * Feeders in loops. */
+int  adhip_stage_begin(adhip_ctx* ctx, int tag);
+int  adhip_stage_write(adhip_ctx* ctx, int tag, uint64_t dst_off, const void* host, size_t bytes);
+int  adhip_stage_end(adhip_ctx* ctx, int tag);
+int  adhip_stage_release(adhip_ctx* ctx, int tag);
+
 /* Stream-ordered device -> device copy inside the arena (capturable). */
 int  adhip_copy(adhip_ctx* ctx, uint64_t dst_off, uint64_t src_off, size_t bytes);
 

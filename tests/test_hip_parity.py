@@ -222,3 +222,25 @@ def test_column_reduce_split(hip, rows, cols):
     ad.execute(device=OracleDevice())
     np.testing.assert_allclose(got["s"], want["s"], rtol=1e-4, atol=1e-4)
     assert np.array_equal(got["m"], want["m"])
+
+
+@pytest.mark.parametrize("iters", [1, 2, 7, 50])
+def test_feeder_values_reach_every_iteration(hip, iters):
+    """A loop accumulates a value fed by the host each iteration (1, 2, ...):
+    the staged copies on the transfer stream must land before, and only
+    before, the iteration that reads them.  The sum is exact in fp32."""
+    holder = [Tensor(np.zeros((4, 64), dtype=np.float32))]
+    count = [0]
+
+    def feed():
+        count[0] += 1
+        return np.full((4, 64), float(count[0]), dtype=np.float32)
+
+    def body():
+        holder[0] += ad.Feeder(feed, shape=[4, 64])
+    ad.ir_for(range(iters), body)
+    got = {}
+    Receiver(lambda v: got.setdefault("acc", v.copy()), [holder[0]])
+    ad.execute(device=hip())
+    assert count[0] == iters
+    assert np.all(got["acc"] == iters * (iters + 1) / 2)
