@@ -54,6 +54,10 @@ struct adhip_ctx {
     hipEvent_t released = nullptr; // on stream: the set's device data is consumed
     bool copied_pending = false, released_pending = false, open = false;
   } tags[kTags];
+  // extra compute streams and an event pool for launch graphs with
+  // parallel branches (stream 0 is `stream`)
+  std::vector<hipStream_t> lanes;
+  std::vector<hipEvent_t> pool;
   std::vector<adhip_module*> modules;
   std::string err;
 };
@@ -136,6 +140,11 @@ void adhip_destroy(adhip_ctx* ctx) {
     if (t.host) hipHostFree(t.host);
   }
   if (ctx->xfer) hipStreamDestroy(ctx->xfer);
+  for (auto st : ctx->lanes) {
+    hipStreamSynchronize(st);
+    hipStreamDestroy(st);
+  }
+  for (auto ev : ctx->pool) hipEventDestroy(ev);
   if (ctx->arena) hipFree(ctx->arena);
   if (ctx->stream) hipStreamDestroy(ctx->stream);
   delete ctx;
@@ -374,6 +383,62 @@ int adhip_launch(adhip_ctx* ctx, void* fn, const uint32_t grid[3], const uint32_
   for (size_t i = 0; i < nargs; ++i) params[i] = (void*)(args + i);
   HIP_TRY(ctx, hipModuleLaunchKernel((hipFunction_t)fn, grid[0], grid[1], grid[2], block[0], block[1],
                                      block[2], shared_bytes, ctx->stream, params, nullptr));
+  return 0;
+}
+
+namespace {
+hipStream_t lane(adhip_ctx* ctx, int s) {
+  if (s == 0) return ctx->stream;
+  if (s < 0 || s > (int)ctx->lanes.size()) return nullptr;
+  return ctx->lanes[s - 1];
+}
+}  // namespace
+
+int adhip_lanes_reserve(adhip_ctx* ctx, int streams, int events) {
+  if (!ctx || streams < 1 || events < 0) return fail(ctx, ADHIP_E_ARG, "bad argument");
+  if (ctx->capturing) return fail(ctx, ADHIP_E_STATE, "lanes_reserve during capture");
+  HIP_TRY(ctx, hipSetDevice(ctx->device));
+  while ((int)ctx->lanes.size() < streams - 1) {
+    hipStream_t st = nullptr;   // default priority
+    HIP_TRY(ctx, hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    ctx->lanes.push_back(st);
+  }
+  while ((int)ctx->pool.size() < events) {
+    hipEvent_t ev = nullptr;
+    HIP_TRY(ctx, hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    ctx->pool.push_back(ev);
+  }
+  return 0;
+}
+
+int adhip_launch_on(adhip_ctx* ctx, int s, void* fn, const uint32_t grid[3], const uint32_t block[3],
+                    uint32_t shared_bytes, const uint64_t* args, size_t nargs) {
+  if (!ctx || !fn || !grid || !block || (nargs && !args)) return fail(ctx, ADHIP_E_ARG, "null argument");
+  hipStream_t st = lane(ctx, s);
+  if (!st) return fail(ctx, ADHIP_E_ARG, "no stream %d", s);
+  if (grid[0] == 0 || grid[1] == 0 || grid[2] == 0) return 0;
+  if (block[0] * block[1] * block[2] > 1024) return fail(ctx, ADHIP_E_ARG, "block too large");
+  void* params[64];
+  if (nargs > 64) return fail(ctx, ADHIP_E_ARG, "too many kernel arguments (%zu)", nargs);
+  for (size_t i = 0; i < nargs; ++i) params[i] = (void*)(args + i);
+  HIP_TRY(ctx, hipModuleLaunchKernel((hipFunction_t)fn, grid[0], grid[1], grid[2], block[0], block[1],
+                                     block[2], shared_bytes, st, params, nullptr));
+  return 0;
+}
+
+int adhip_record_on(adhip_ctx* ctx, int s, int ev) {
+  if (!ctx) return fail(ctx, ADHIP_E_ARG, "null ctx");
+  hipStream_t st = lane(ctx, s);
+  if (!st || ev < 0 || ev >= (int)ctx->pool.size()) return fail(ctx, ADHIP_E_ARG, "bad stream %d / event %d", s, ev);
+  HIP_TRY(ctx, hipEventRecord(ctx->pool[ev], st));
+  return 0;
+}
+
+int adhip_wait_on(adhip_ctx* ctx, int s, int ev) {
+  if (!ctx) return fail(ctx, ADHIP_E_ARG, "null ctx");
+  hipStream_t st = lane(ctx, s);
+  if (!st || ev < 0 || ev >= (int)ctx->pool.size()) return fail(ctx, ADHIP_E_ARG, "bad stream %d / event %d", s, ev);
+  HIP_TRY(ctx, hipStreamWaitEvent(st, ctx->pool[ev], 0));
   return 0;
 }
 

@@ -12,8 +12,10 @@ replays loop bodies, ``execute`` runs both passes.  Differences by design:
   text and compiled in parallel through hipRTC at the end of the init pass;
   every kernel reads its arguments from a row of an argument table;
 * each stretch of commands between Feeders/Receivers/loops is scheduled
-  (``schedule``): launches ordered by their memory conflicts, and
-  independent launches of one kernel merged into one launch;
+  (``schedule``): launches ordered by their memory conflicts, independent
+  launches of one kernel merged into one launch; the groups can be spread
+  over several streams with event edges only where they touch overlapping
+  memory (``lanes``; one stream by default, see ``__init__``);
 * a loop body without Receivers is captured once as a HIP graph and the
   graph is replayed ``len(r)`` times; a Feeder inside it copies from one of
   two staging slots, which the host refills on a transfer stream while the
@@ -37,7 +39,7 @@ from ...node import Node
 from .. import Device
 from . import codegen
 from .runtime import HEADER_PATH, Context, compile_source
-from .schedule import schedule
+from .schedule import assign_lanes, schedule_dag
 
 ALIGN = 256
 SCRATCH_RING_FLOATS = 64 << 20     # 256 MiB of scratch slots for multi-pass commands
@@ -65,7 +67,7 @@ class _Launch:
 
 class HIPDevice(Device):
     def __init__(self, device_index: int = 0, use_graphs: bool = True, jit_threads: int = None,
-                 group_launches: bool = True):
+                 group_launches: bool = True, lanes: int = 1):
         super().__init__()
         self.kernels = {}            # program_id -> [KernelPlan]
         self.funcs = {}              # program_id -> launch callable (ungrouped)
@@ -73,6 +75,13 @@ class HIPDevice(Device):
         self.buffers_size = {}       # buffer id -> floats
         self.use_graphs = use_graphs
         self.group_launches = group_launches
+        # parallel streams for independent launch groups.  One by default:
+        # capturing the C4 training step on four lanes ended in a host
+        # segmentation fault inside hipStreamEndCapture/hipGraphInstantiate
+        # whose cause is not established; with one lane the schedule has no
+        # events and is the plain in-order capture.
+        self.lanes = max(1, lanes)
+        self._events = 0             # event pool entries used by the schedules
         self.jit_threads = jit_threads or min(16, (os.cpu_count() or 4))
         self.ctx = Context(device_index)
         self._allocs = []
@@ -193,16 +202,17 @@ class HIPDevice(Device):
             self.kernels[pid] = ps
             self.stats["kernels"] += len(ps)
             self.funcs[pid] = launches[0] if len(launches) == 1 else (lambda ls=launches: [f() for f in ls])
+        self.ctx.lanes_reserve(self.lanes, self._events)
         for pid_proc, items in sched.items():
             out = []
             for item in items:
-                if item[0] == "cmd":
+                if item[0] in ("cmd", "record", "wait"):
                     out.append(item)
                     continue
-                _, plan, row, count = item
+                _, plan, row, count, lane = item
                 grid = (plan.grid[0], plan.grid[1], count)
-                out.append(("launch", self.ctx.launcher(funcs[plan.name], grid, plan.block, plan.shared,
-                                                        [tbase + row])))
+                go = self.ctx.launcher_on(funcs[plan.name], grid, plan.block, plan.shared, [tbase + row])
+                out.append(("launch", go, lane))
             self._schedules[pid_proc] = out
         self._pending = []
 
@@ -246,11 +256,30 @@ class HIPDevice(Device):
                         launches.append(_Launch(cmd, plan, None, reads, writes))
                 key = (lambda L: (L.plan.name, L.plan.grid, L.plan.block, L.plan.shared)) \
                     if self.group_launches else (lambda L: None)
-                for group in schedule([(L, L.reads, L.writes) for L in launches], key):
+                groups, deps = schedule_dag([(L, L.reads, L.writes) for L in launches], key)
+                lane_of, waits = assign_lanes(deps, self.lanes)
+                # fork the lanes this stretch uses off stream 0, join them back at its end
+                used = sorted(set(lane_of) - {0})
+                if used:
+                    fork = self._new_event()
+                    items.append(("record", 0, fork))
+                    items.extend(("wait", lane, fork) for lane in used)
+                recorded = {}
+                needed = {d for w in waits for d in w}
+                for g, group in enumerate(groups):
+                    for d in waits[g]:
+                        items.append(("wait", lane_of[g], recorded[d]))
                     members = [launches[i] for i in group]
                     plan = members[0].plan
                     row = add_rows([self._arg_values(m.plan, m.cmd.program_id) for m in members])
-                    items.append(("launch", plan, row, len(members)))
+                    items.append(("launch", plan, row, len(members), lane_of[g]))
+                    if g in needed:
+                        recorded[g] = self._new_event()
+                        items.append(("record", lane_of[g], recorded[g]))
+                for lane in used:
+                    join = self._new_event()
+                    items.append(("record", lane, join))
+                    items.append(("wait", 0, join))
                 stretch.clear()
 
             for cmd in p.procedure:
@@ -268,6 +297,10 @@ class HIPDevice(Device):
 
         visit(proc)
         return out
+
+    def _new_event(self):
+        self._events += 1
+        return self._events - 1
 
     def _compile(self, plans):
         """hipRTC-compile every distinct kernel (in parallel) and load it."""
@@ -325,9 +358,15 @@ class HIPDevice(Device):
         return not any(isinstance(c, (Receiver, ForNode)) for c in proc.procedure)
 
     def _run_scheduled(self, proc):
+        ctx = self.ctx
         for item in self._schedules[proc.id]:
-            if item[0] == "launch":
-                item[1]()
+            kind = item[0]
+            if kind == "launch":
+                item[1](item[2])
+            elif kind == "record":
+                ctx.record_on(item[1], item[2])
+            elif kind == "wait":
+                ctx.wait_on(item[1], item[2])
             elif isinstance(item[1], ForNode):
                 self._run_loop(item[1])
             else:
@@ -402,8 +441,9 @@ class HIPDevice(Device):
         self._run_proc(proc, self.init, init=True)
         self._finish_init(proc)
         for loop in self.loops(proc):
-            self.stats["launches_per_iter"] = sum(1 for it in self._schedules[loop.get_proc().id]
-                                                  if it[0] == "launch")
+            items = self._schedules[loop.get_proc().id]
+            self.stats["launches_per_iter"] = sum(1 for it in items if it[0] == "launch")
+            self.stats["lanes_used"] = len({it[2] for it in items if it[0] == "launch"})
 
     def execute(self, proc):
         self.prepare(proc)

@@ -21,7 +21,7 @@ EXPORTS = [
     "adhip_read", "adhip_copy", "adhip_compile", "adhip_free", "adhip_module_load",
     "adhip_module_function", "adhip_launch", "adhip_graph_begin", "adhip_graph_end",
     "adhip_graph_launch", "adhip_graph_destroy", "adhip_sync", "adhip_event_record",
-    "adhip_event_elapsed",
+    "adhip_event_elapsed", "adhip_lanes_reserve", "adhip_launch_on", "adhip_record_on", "adhip_wait_on",
 ]
 
 
@@ -65,6 +65,10 @@ def load_library(path=LIB_PATH):
             "adhip_sync": (i32, [vp]),
             "adhip_event_record": (i32, [vp, i32]),
             "adhip_event_elapsed": (i32, [vp, i32, i32, c.POINTER(c.c_float)]),
+            "adhip_lanes_reserve": (i32, [vp, i32, i32]),
+            "adhip_launch_on": (i32, [vp, i32, vp, c.POINTER(u32), c.POINTER(u32), u32, c.POINTER(u64), sz]),
+            "adhip_record_on": (i32, [vp, i32, i32]),
+            "adhip_wait_on": (i32, [vp, i32, i32]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(lib, name)
@@ -181,6 +185,32 @@ class Context:
             if rc != 0:
                 check(rc, "adhip_launch")
         return go
+
+    def lanes_reserve(self, streams: int, events: int):
+        self.check(self.lib.adhip_lanes_reserve(self.h, streams, events), "adhip_lanes_reserve")
+
+    def launcher_on(self, fn, grid, block, shared, args):
+        """A callable ``go(stream)`` launching ``fn`` on a lane with fixed
+        arguments."""
+        g = (ctypes.c_uint32 * 3)(*grid)
+        b = (ctypes.c_uint32 * 3)(*block)
+        a = (ctypes.c_uint64 * max(1, len(args)))(*[int(v) & 0xFFFFFFFFFFFFFFFF for v in args])
+        n = len(args)
+        launch = self.lib.adhip_launch_on
+        h = self.h
+        check = self.check
+
+        def go(stream=0):
+            rc = launch(h, stream, fn, g, b, shared, a, n)
+            if rc != 0:
+                check(rc, "adhip_launch_on")
+        return go
+
+    def record_on(self, stream: int, event: int):
+        self.check(self.lib.adhip_record_on(self.h, stream, event), "adhip_record_on")
+
+    def wait_on(self, stream: int, event: int):
+        self.check(self.lib.adhip_wait_on(self.h, stream, event), "adhip_wait_on")
 
     def graph_begin(self):
         self.check(self.lib.adhip_graph_begin(self.h), "adhip_graph_begin")

@@ -95,6 +95,19 @@ int  adhip_module_function(adhip_module* mod, const char* name, void** fn);
 int  adhip_launch(adhip_ctx* ctx, void* fn, const uint32_t grid[3], const uint32_t block[3],
                   uint32_t shared_bytes, const uint64_t* args, size_t nargs);
 
+/* Parallel launch lanes: `streams` compute streams in all (stream 0 is the
+ * context stream; the others are created at default priority) and a pool of
+ * `events` events.  launch_on / record_on / wait_on put a launch, an event
+ * record or an event wait on a lane, so a captured graph gets parallel
+ * branches with edges only where launches touch overlapping memory.  The
+ * reference enqueues every command on one in-order queue
+ * (cl_helper.py:128-139). */
+int  adhip_lanes_reserve(adhip_ctx* ctx, int streams, int events);
+int  adhip_launch_on(adhip_ctx* ctx, int stream, void* fn, const uint32_t grid[3], const uint32_t block[3],
+                     uint32_t shared_bytes, const uint64_t* args, size_t nargs);
+int  adhip_record_on(adhip_ctx* ctx, int stream, int event);
+int  adhip_wait_on(adhip_ctx* ctx, int stream, int event);
+
 /* Record the context stream's work between begin and end as a HIP graph,
  * then replay it.  The reference replays a loop body by re-enqueueing
  * every command from Python (device.py:121-129). */

@@ -124,3 +124,41 @@ def test_scheduled_order_gives_identical_results(build):
         assert moved > 0          # the schedule really reorders this program
     for a, b in zip(want["params"], got["params"]):
         assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("seed", range(25))
+def test_dag_lanes_order_every_conflict(seed):
+    """Running the groups on lanes, each lane in order and waiting only for
+    the recorded cross-lane dependencies, orders every conflicting pair of
+    launches as in program order (checked through the happens-before
+    closure of lane order plus waits)."""
+    from ad_amd.device.hip.schedule import assign_lanes, schedule_dag
+    rng = random.Random(seed)
+    launches = []
+    for i in range(rng.randint(1, 60)):
+        def rnd():
+            out = []
+            for _ in range(rng.randint(0, 3)):
+                lo = rng.randint(0, 40)
+                out.append((rng.choice("ab"), lo, lo + rng.randint(0, 12)))
+            return out
+        launches.append((rng.choice("xyz"), rnd(), rnd()))
+    groups, deps = schedule_dag(launches, group_key=lambda item: item)
+    lane_of, waits = assign_lanes(deps, 4)
+    n = len(groups)
+    before = [set() for _ in range(n)]          # groups finished before g starts
+    last = {}
+    for g in range(n):
+        s = lane_of[g]
+        preds = set(waits[g])
+        if s in last:
+            preds.add(last[s])
+        for p in preds:
+            before[g] |= before[p] | {p}
+        last[s] = g
+    group_of = {i: g for g, m in enumerate(groups) for i in m}
+    for i in range(len(launches)):
+        for j in range(i + 1, len(launches)):
+            if _conflict(launches[i], launches[j]):
+                gi, gj = group_of[i], group_of[j]
+                assert gi != gj and gi in before[gj], (i, j)
