@@ -244,3 +244,22 @@ def test_feeder_values_reach_every_iteration(hip, iters):
     ad.execute(device=hip())
     assert count[0] == iters
     assert np.all(got["acc"] == iters * (iters + 1) / 2)
+
+
+@pytest.mark.parametrize("ta", [False, True])
+def test_dotprod_partial_tile_rows(hip, ta):
+    """A partial last row of tiles (M = 4160) in a large product."""
+    M, K, N = 4160, 256, 4096
+    rng = np.random.default_rng(11)
+    a = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    b = rng.standard_normal((K, N)).astype(np.float32)
+    A = Tensor(a)
+    r = (A.T() if ta else A) @ Tensor(b)
+    got = {}
+    Receiver(lambda v: got.setdefault("r", v.copy()), [r])
+    ad.execute(device=hip())
+    aa = (a.T if ta else a).astype(np.float64)
+    rows = np.concatenate([np.arange(0, 64), np.arange(M - 128, M)])
+    ref = aa[rows] @ b.astype(np.float64)
+    bound = 4 * K * np.finfo(np.float32).eps * (np.abs(a).max() * np.abs(b).max())
+    np.testing.assert_allclose(got["r"][rows], ref, rtol=0, atol=bound)
