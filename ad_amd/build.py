@@ -38,7 +38,13 @@ struct LA { static constexpr int kMode = 0; static constexpr bool kVec = true; f
 struct LB { static constexpr int kMode = 1; static constexpr bool kVec = false; float* p0;
   __device__ float at(unsigned x, unsigned y) const { return p0[y * 64u + x]; }
   __device__ float4 at4(unsigned x, unsigned y) const { return *reinterpret_cast<const float4*>(p0 + y * 64u + x); } };
-struct EPI { float* p0; __device__ void operator()(float v, unsigned x, unsigned y, int c) const { p0[(c * 64u + x) * 64u + y] = v; } };
+struct EPI { float* p0; static constexpr bool kVec4 = false; static constexpr int kLoads = 1;
+  __device__ void load(unsigned x, unsigned y, float* l) const { l[0] = p0[x * 64u + y]; }
+  __device__ void operator()(float v, unsigned x, unsigned y, int c, const float* l) const { p0[(c * 64u + x) * 64u + y] = v + l[0]; } };
+struct EP4 { float* p0; static constexpr bool kVec4 = true; static constexpr int kLoads = 1;
+  __device__ void load4(unsigned x, unsigned y, float4* l) const { l[0] = *reinterpret_cast<const float4*>(p0 + x * 64u + y); }
+  __device__ void vec(float4 v, unsigned x, unsigned y, int c, const float4* l) const {
+    *reinterpret_cast<float4*>(p0 + (c * 64u + x) * 64u + y) = make_float4(v.x + l[0].x, v.y + l[0].y, v.z + l[0].z, v.w + l[0].w); } };
 struct LD { static constexpr bool kVec = true; float* p0;
   __device__ float at(unsigned x, unsigned y) const { return p0[x * 64u + y]; }
   __device__ float4 at4(unsigned x, unsigned y) const { return *reinterpret_cast<const float4*>(p0 + x * 64u + y); }
@@ -47,6 +53,8 @@ struct EPR { float* p0; __device__ void operator()(float v, unsigned x, int c) c
 extern "C" __global__ void __launch_bounds__(256) probe_dp(float* a) { adhip::dp_mfma<128, 128, 1>(LA{a}, LB{a}, EPI{a}, 64, 64, 64); }
 extern "C" __global__ void __launch_bounds__(256) probe_dp_narrow(float* a) { adhip::dp_mfma<128, 64, 4>(LA{a}, LB{a}, EPI{a}, 64, 64, 64); }
 extern "C" __global__ void __launch_bounds__(256) probe_dp_small(float* a) { adhip::dp_mfma<64, 64, 2>(LA{a}, LB{a}, EPI{a}, 64, 64, 64); }
+extern "C" __global__ void __launch_bounds__(256) probe_dp_vec(float* a) { adhip::dp_mfma<128, 64, 1>(LA{a}, LB{a}, EP4{a}, 64, 64, 64); }
+extern "C" __global__ void __launch_bounds__(256) probe_dp_vec_small(float* a) { adhip::dp_mfma<64, 64, 4>(LA{a}, LB{a}, EP4{a}, 64, 64, 64); }
 extern "C" __global__ void __launch_bounds__(256) probe_rr(float* a) { adhip::reduce_rows<0>(LD{a}, EPR{a}, 64u, 64u, false); }
 extern "C" __global__ void __launch_bounds__(256) probe_rc(float* a) { adhip::reduce_cols<1, 1>(LD{a}, EPR{a}, 64u, 64u, true); }
 extern "C" __global__ void __launch_bounds__(256) probe_rcs(float* a) { adhip::reduce_cols<0, 8>(LD{a}, EPR{a}, 64u, 64u, false); }

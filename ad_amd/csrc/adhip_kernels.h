@@ -37,8 +37,15 @@ __device__ __forceinline__ float rop(float a, float b) {
 // consumed, then stored into the other buffer.
 // SPLIT > 1 splits K into SPLIT chunks: blockIdx.y = tile row + tiles_m *
 // chunk, and the epilogue receives the chunk index (partial results).
-// The epilogue is called as epi(value, row, col, chunk) in registers.
-constexpr int DP_BK = 16, DP_PAD = 4, DP_GROUP = 8;
+// Epilogue, EPI::kVec4 false: per 32x32 tile, epi.load(row, col, l) fills
+// the operand registers l[EPI::kLoads] of all 16 values of a lane, then
+// epi(value, row, col, chunk, l) runs the statements of each.
+// EPI::kVec4 true (N a multiple of 4): each wave passes its 32x32 tiles
+// through LDS so a lane holds 4 consecutive columns of a row; per tile,
+// epi.load4(row, col, l) fills float4 operand registers for the lane's 4
+// groups, then epi.vec(value4, row, col, chunk, l) runs the statements on 4
+// elements with float4 loads and stores.
+constexpr int DP_BK = 16, DP_PAD = 4, DP_GROUP = 8, DP_CPITCH = 40;
 
 template <int BM, int BN, int SPLIT, class LA, class LB, class EPI>
 __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& epi, int M, int N, int K) {
@@ -47,8 +54,14 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
   constexpr int VA = BM * DP_BK / 4 / 256;               // float4 loads per thread
   constexpr int VB = BN * DP_BK / 4 / 256;
   static_assert(VA >= 1 && VB >= 1, "tile too small for 256 threads");
-  __shared__ float As[2][DP_BK][BM + DP_PAD];
-  __shared__ float Bs[2][DP_BK][BN + DP_PAD];
+  // K panels (two buffers of A and of B) and, after the products, the
+  // per-wave 32x32 staging of the vectorised epilogue share one LDS block
+  constexpr int A_FLOATS = 2 * DP_BK * (BM + DP_PAD), B_FLOATS = 2 * DP_BK * (BN + DP_PAD);
+  constexpr int C_FLOATS = EPI::kVec4 ? 4 * 32 * DP_CPITCH : 0;
+  constexpr int S_FLOATS = A_FLOATS + B_FLOATS > C_FLOATS ? A_FLOATS + B_FLOATS : C_FLOATS;
+  __shared__ __attribute__((aligned(16))) float smem[S_FLOATS];
+  float (*As)[DP_BK][BM + DP_PAD] = reinterpret_cast<float (*)[DP_BK][BM + DP_PAD]>(smem);
+  float (*Bs)[DP_BK][BN + DP_PAD] = reinterpret_cast<float (*)[DP_BK][BN + DP_PAD]>(smem + A_FLOATS);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -205,17 +218,57 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
     }
   }
   // 32x32 accumulator layout: lane holds column (lane % 32) and rows
-  // 8*(r/4) + 4*(lane/32) + r%4 for r = 0..15
+  // 8*(r/4) + 4*(lane/32) + r%4 for r = 0..15.  Per 32x32 tile, the
+  // epilogue's operand loads for all 16 values are issued first, then the
+  // statements run.
+  constexpr int NL = EPI::kLoads > 0 ? EPI::kLoads : 1;
+  if constexpr (EPI::kVec4) {
+    // lane -> row 8*q + lane/8 and columns 4*(lane%8) .. +3 of the tile
+    __syncthreads();
+    float* cs = smem + wave * 32 * DP_CPITCH;
+    const int qr = lane >> 3, qc = 4 * (lane & 7);
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
+      for (int j = 0; j < TN; ++j) {
+        const int col = n0 + wn * (BN / 2) + j * 32 + qc;
+        const int rbase = m0 + wm * (BM / 2) + i * 32 + qr;
+        float4 lv[4][NL];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
-        const int col = n0 + wn * (BN / 2) + j * 32 + lr;
-        if (row < M && col < N) epi(acc[i][j][r], row, col, chunk);
+        for (int q = 0; q < 4; ++q)
+          if (rbase + 8 * q < M && col < N) epi.load4(rbase + 8 * q, col, lv[q]);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) cs[(8 * (r >> 2) + 4 * lk + (r & 3)) * DP_CPITCH + lr] = acc[i][j][r];
+        // lanes read what other lanes of the wave wrote (LDS executes a
+        // wave's operations in order; the fences keep the compiler's order)
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        float4 v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = *reinterpret_cast<const float4*>(cs + (8 * q + qr) * DP_CPITCH + qc);
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (rbase + 8 * q < M && col < N) epi.vec(v[q], rbase + 8 * q, col, chunk, lv[q]);
       }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        float lv[16][NL];
+        const int col = n0 + wn * (BN / 2) + j * 32 + lr;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+          if (row < M && col < N) epi.load(row, col, lv[r]);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+          if (row < M && col < N) epi(acc[i][j][r], row, col, chunk, lv[r]);
+        }
+      }
+  }
 }
 
 // ---------------------------------------------------------------- Reduce+Elw

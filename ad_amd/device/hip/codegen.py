@@ -385,14 +385,90 @@ def _scratch_km(off, access=None):
     return km
 
 
-class Lowerer:
-    """Emits scalar C++ for operands and statements of one kernel."""
+HOIST_MAX = 8
+_NO_SIZES = BufferInfo()
 
-    def __init__(self, ity, params: Params):
+
+class _StoreTracker:
+    """The regions one element has stored to so far, and the operand reads
+    hoisted ahead of every store (``_l[k]``, up to ``limit`` of them)."""
+
+    def __init__(self, limit):
+        self.limit = limit
+        self.stored: List[tuple] = []
+        self.scratch_stored = False
+        self.loads: List[str] = []
+        self._idx: Dict[str, int] = {}
+
+    def free(self, karg) -> bool:
+        """True if no store so far may have written what ``karg`` reads."""
+        if isinstance(karg, KConcat):
+            return self.free(karg.karg_one) and self.free(karg.karg_two)
+        if not isinstance(karg, KMatrix) or karg.is_temp:
+            return False
+        if getattr(karg, "scratch_offset", None) is not None:
+            return not self.scratch_stored
+        buf, lo, hi = _region(karg, _NO_SIZES)[0]
+        return not any(b == buf and lo < h and l < hi for b, l, h in self.stored)
+
+    def hoisted(self, expr):
+        """``_l[k]`` for ``expr`` (one slot per distinct expression), or None
+        when the slots are used up."""
+        if expr not in self._idx:
+            if len(self.loads) >= self.limit:
+                return None
+            self._idx[expr] = len(self.loads)
+            self.loads.append(expr)
+        return f"_l[{self._idx[expr]}]"
+
+    def note(self, km):
+        if getattr(km, "scratch_offset", None) is not None:
+            self.scratch_stored = True
+        else:
+            self.stored.append(_region(km, _NO_SIZES)[0])
+
+
+class Lowerer:
+    """Emits scalar C++ for operands and statements of one kernel.
+
+    With ``hoist`` the operand reads that no earlier store of the same
+    element can reach (no store so far overlaps their region) become
+    ``_l[k]``, and ``loads`` lists the expressions that fill ``_l``: the
+    caller evaluates them for a batch of elements before running any of
+    their statements, so the loads are in flight together instead of each
+    waiting behind the previous element's stores (which may alias them as
+    far as the compiler knows).  Elements never touch each other's
+    locations within one pass (cross-element conflicts split passes), so
+    only the element's own earlier stores matter."""
+
+    def __init__(self, ity, params: Params, hoist=False):
         self.ity = ity
         self.params = params
         self.forward: Dict[tuple, str] = {}   # location key -> register holding its value
         self.nreg = 0
+        self.hoist = hoist
+        self.stores = _StoreTracker(HOIST_MAX)
+
+    @property
+    def loads(self) -> List[str]:
+        return self.stores.loads
+
+    def _free(self, karg) -> bool:
+        return self.stores.free(karg)
+
+    def _hoisted(self, expr) -> str:
+        return self.stores.hoisted(expr)
+
+    def _note_store(self, km):
+        self.stores.note(km)
+
+    @property
+    def _scratch_stored(self):
+        return self.stores.scratch_stored
+
+    @_scratch_stored.setter
+    def _scratch_stored(self, v):
+        self.stores.scratch_stored = v
 
     def _loc(self, km: KMatrix):
         core, c = split_const(km.access)
@@ -406,6 +482,13 @@ class Lowerer:
     def operand(self, karg) -> str:
         if isinstance(karg, KConstant):
             return const_literal(karg.constant)
+        if self.hoist and self._free(karg):
+            self.hoist = False
+            try:
+                expr = self.operand(karg)
+            finally:
+                self.hoist = True
+            return self._hoisted(expr) or expr
         if isinstance(karg, KConcat):
             cond = lower_index(karg.condition, self.ity)
             return f"({cond} ? ({self.operand(karg.karg_two)}) : ({self.operand(karg.karg_one)}))"
@@ -451,11 +534,15 @@ class Lowerer:
                 continue
             if kind == "load":          # temp carried in from an earlier pass
                 tid, off = n
-                lines.append(f"float temp_{tid} = {self.params.ptr('scratch', 0, off)}[_global_id];")
+                expr = f"{self.params.ptr('scratch', 0, off)}[_global_id]"
+                if self.hoist and not self._scratch_stored:
+                    expr = self._hoisted(expr) or expr
+                lines.append(f"float temp_{tid} = {expr};")
                 continue
             if kind == "store":         # temp carried out to a later pass
                 tid, off = n
                 lines.append(f"{self.params.ptr('scratch', 0, off)}[_global_id] = temp_{tid};")
+                self._scratch_stored = True
                 continue
             if kind == "sum":           # combine the chunk results of a split pass, in order
                 off, chunks, count, op, pad_zero = n
@@ -477,6 +564,7 @@ class Lowerer:
             p, idx, key = self._loc(n.kres)
             lines.append(f"{p}[{idx}] = {r};")
             self.forward[key] = r
+            self._note_store(n.kres)
         return lines
 
 
@@ -600,6 +688,21 @@ def _vector_source(stmts, ity, params: Params, setup="", index_kind="global") ->
     """Four consecutive elements per thread: float4 loads/stores for aligned
     contiguous accesses, one scalar load for group-constant accesses, a
     concat evaluated once per group (its condition is group-constant)."""
+    body = "\n  ".join(_vector_lines(stmts, ity, params, index_kind))
+    return f"""extern "C" __global__ void __launch_bounds__({BLOCK}) {KNAME}({_params_decl(params)}{', ' if params.slots else ''}unsigned long long n_) {{
+  const {ity} _global_id = (({ity})blockIdx.x * {BLOCK}u + threadIdx.x) * 4u;
+  if (_global_id >= ({ity})n_) return;
+  {setup}
+  {body}
+}}
+"""
+
+
+def _vector_lines(stmts, ity, params: Params, index_kind="global", hoist=None) -> List[str]:
+    """Statement lines for four consecutive elements ``_global_id`` ..
+    ``_global_id + 3`` (``_global_id`` a multiple of 4).  With ``hoist`` (a
+    ``_StoreTracker``) the reads no earlier store of the group can reach
+    become float4 slots ``_l[k]`` whose expressions go to ``hoist.loads``."""
     lines = []
     loaded: Dict[tuple, List[str]] = {}
     written: Dict[tuple, str] = {}
@@ -650,8 +753,15 @@ def _vector_source(stmts, ity, params: Params, setup="", index_kind="global") ->
                 return [f"{written[key]}.{c}" for c in "xyzw"]
             if key in loaded:
                 return loaded[key]
+        expr = vec_expr(k)
+        slot = hoist.hoisted(expr) if hoist is not None and hoist.free(k) else None
+        if slot is not None:
+            vals = [f"{slot}.{c}" for c in "xyzw"]
+            if isinstance(k, KMatrix):
+                loaded[loc(k)[2]] = vals
+            return vals
         v = fresh("v")
-        lines.append(f"const float4 {v} = {vec_expr(k)};")
+        lines.append(f"const float4 {v} = {expr};")
         vals = [f"{v}.{c}" for c in "xyzw"]
         if isinstance(k, KMatrix):
             loaded[loc(k)[2]] = vals
@@ -689,14 +799,19 @@ def _vector_source(stmts, ity, params: Params, setup="", index_kind="global") ->
             continue
         if kind == "load":
             tid, off = n
-            v = fresh("v")
-            lines.append(f"const float4 {v} = *reinterpret_cast<const float4*>({params.ptr('scratch', 0, off)} + _global_id);")
+            expr = f"(*reinterpret_cast<const float4*>({params.ptr('scratch', 0, off)} + _global_id))"
+            v = hoist.hoisted(expr) if hoist is not None and not hoist.scratch_stored else None
+            if v is None:
+                v = fresh("v")
+                lines.append(f"const float4 {v} = {expr};")
             lines.append(f"float temp_{tid}[4] = {{{v}.x, {v}.y, {v}.z, {v}.w}};")
             continue
         if kind == "store":
             tid, off = n
             lines.append(f"*reinterpret_cast<float4*>({params.ptr('scratch', 0, off)} + _global_id) = "
                          f"make_float4(temp_{tid}[0], temp_{tid}[1], temp_{tid}[2], temp_{tid}[3]);")
+            if hoist is not None:
+                hoist.scratch_stored = True
             continue
         if kind == "sum":
             off, chunks, count, op, pad_zero = n
@@ -727,14 +842,9 @@ def _vector_source(stmts, ity, params: Params, setup="", index_kind="global") ->
         lines.append(f"*reinterpret_cast<float4*>({p} + {lower_index(core, ity)}) = {r};")
         written[key] = r
         loaded.pop(key, None)
-    body = "\n  ".join(lines)
-    return f"""extern "C" __global__ void __launch_bounds__({BLOCK}) {KNAME}({_params_decl(params)}{', ' if params.slots else ''}unsigned long long n_) {{
-  const {ity} _global_id = (({ity})blockIdx.x * {BLOCK}u + threadIdx.x) * 4u;
-  if (_global_id >= ({ity})n_) return;
-  {setup}
-  {body}
-}}
-"""
+        if hoist is not None:
+            hoist.note(n.kres)
+    return lines
 
 
 # ------------------------------------------------------------------ DotProd+Elw family
@@ -788,14 +898,16 @@ def _init_list(params: Params) -> str:
 
 def dp_config(M, N, K):
     """Block tile and K split of a DotProd: 64-wide tiles on a narrow side,
-    128 otherwise (256 x 128 measured slower at 4096^3 and in the C5 step);
+    128 otherwise (256 x 128 measured slower at 4096^3 and in the C5 step),
+    and 64 x 64 for a short K (<= 128), where the epilogue's HBM traffic
+    dominates and more, smaller blocks keep more of it in flight;
     K is split (up to 16 chunks of at least 256) while the
     tiles alone would not give one block per compute unit, and a long K
     (chunks of at least 1024) is split once more until two blocks share
     each compute unit (one block's barriers then hide behind the other's
     products)."""
-    BM = 64 if M <= 64 else 128
-    BN = 64 if N <= 64 else 128
+    BM = 64 if M <= 64 or K <= 128 else 128
+    BN = 64 if N <= 64 or K <= 128 else 128
     tiles = ceil(M / BM) * ceil(N / BN)
     split = 1
     while tiles * split < 256 and split < 16 and K // (2 * split) >= 256:
@@ -803,6 +915,22 @@ def dp_config(M, N, K):
     while tiles * split < 512 and split < 16 and K // (2 * split) >= 1024:
         split *= 2
     return BM, BN, split
+
+
+VEC_HOIST_MAX = 4
+
+
+def epilogue_vec_ok(stmts, M, N) -> bool:
+    """The in-kernel epilogue of an M x N DotProd can run on groups of 4
+    consecutive columns: every access it makes (the product's own store
+    included) is contiguous and 4-aligned along the row, or constant over
+    the group."""
+    if N % 4 != 0 or not stmts:
+        return False
+    for kind, node in stmts:
+        if kind == "init" and not node.kres.is_temp and not _vec_access_ok(node.kres, "dp", True):
+            return False
+    return _vector_plan([st for st in stmts if st[0] != "init"], M * N, "dp", N)
 
 
 def dotprod_plan(stmts, dp, A=None, B=None, config=None, partial_off=None) -> KernelPlan:
@@ -822,16 +950,46 @@ def dotprod_plan(stmts, dp, A=None, B=None, config=None, partial_off=None) -> Ke
     params = Params()
     la, _ = _loader_struct("LA", A, "A", params, ity, (M, K))
     lb, _ = _loader_struct("LB", B, "B", params, ity, (K, N))
+    gid = f"const {ity} _global_id = _x * ({ity}){N} + _y; (void)_global_id;"
     if partial_off is not None:
         assert not stmts, "a DotProd storing partial products runs no epilogue"
-        pp = params.ptr("scratch", 0, partial_off)
-        body = (f"{pp}[((unsigned long long)_chunk * {M}ull + _x) * {N}ull + _y] = _value;")
+    vec4 = N % 4 == 0 and (partial_off is not None or epilogue_vec_ok(stmts, M, N))
+    if vec4:
+        # four consecutive columns per call, float4 loads and stores
+        if partial_off is not None:
+            pp = params.ptr("scratch", 0, partial_off)
+            lines, loads = [f"*reinterpret_cast<float4*>({pp} + ((unsigned long long)_chunk * {M}ull + _x) * "
+                            f"{N}ull + _y) = _value;"], []
+        else:
+            tracker = _StoreTracker(VEC_HOIST_MAX)
+            lines = _vector_lines(stmts, ity, params, "dp", hoist=tracker)
+            loads = tracker.loads
+        body = "\n    ".join(lines)
+        fill = "".join(f"\n    _l[{i}] = {e};" for i, e in enumerate(loads))
+        epi = (f"struct EPI {{ @FIELDS@\n"
+               f"  static constexpr bool kVec4 = true;\n"
+               f"  static constexpr int kLoads = {len(loads)};\n"
+               f"  __device__ void load4({ity} _x, {ity} _y, float4* _l) const {{\n"
+               f"    {gid} (void)_l;{fill}\n  }}\n"
+               f"  __device__ void vec(float4 _value, {ity} _x, {ity} _y, int _chunk, const float4* _l) const {{\n"
+               f"    {gid} (void)_chunk; (void)_l;\n    {body}\n  }} }};\n")
     else:
-        low = Lowerer(ity, params)
-        body = "\n    ".join(low.statements(stmts, "_value"))
-    epi = (f"struct EPI {{ @FIELDS@\n"
-           f"  __device__ void operator()(float _value, {ity} _x, {ity} _y, int _chunk) const {{\n"
-           f"    const {ity} _global_id = _x * ({ity}){N} + _y; (void)_global_id; (void)_chunk;\n    {body}\n  }} }};\n")
+        loads = []
+        if partial_off is not None:
+            pp = params.ptr("scratch", 0, partial_off)
+            body = (f"{pp}[((unsigned long long)_chunk * {M}ull + _x) * {N}ull + _y] = _value;")
+        else:
+            low = Lowerer(ity, params, hoist=True)
+            body = "\n    ".join(low.statements(stmts, "_value"))
+            loads = low.loads
+        fill = "".join(f"\n    _l[{i}] = {e};" for i, e in enumerate(loads))
+        epi = (f"struct EPI {{ @FIELDS@\n"
+               f"  static constexpr bool kVec4 = false;\n"
+               f"  static constexpr int kLoads = {len(loads)};\n"
+               f"  __device__ void load({ity} _x, {ity} _y, float* _l) const {{\n"
+               f"    {gid} (void)_l;{fill}\n  }}\n"
+               f"  __device__ void operator()(float _value, {ity} _x, {ity} _y, int _chunk, const float* _l) const {{\n"
+               f"    {gid} (void)_chunk; (void)_l;\n    {body}\n  }} }};\n")
     init = _init_list(params)
     src = ((la + lb + epi).replace("@FIELDS@", _fields(params)) +
            f"extern \"C\" __global__ void __launch_bounds__(256) {KNAME}({_params_decl(params)}) {{\n"

@@ -75,11 +75,11 @@ class HIPDevice(Device):
         self.buffers_size = {}       # buffer id -> floats
         self.use_graphs = use_graphs
         self.group_launches = group_launches
-        # parallel streams for independent launch groups.  One by default:
-        # capturing the C4 training step on four lanes ended in a host
-        # segmentation fault inside hipStreamEndCapture/hipGraphInstantiate
-        # whose cause is not established; with one lane the schedule has no
-        # events and is the plain in-order capture.
+        # parallel streams for independent launch groups in uncaptured runs
+        # (eager launches).  Graph capture always uses one lane: capturing
+        # the C4 training step on four lanes ended in a host segmentation
+        # fault inside hipStreamEndCapture/hipGraphInstantiate whose cause is
+        # not established.
         self.lanes = max(1, lanes)
         self._events = 0             # event pool entries used by the schedules
         self.jit_threads = jit_threads or min(16, (os.cpu_count() or 4))
@@ -91,7 +91,8 @@ class HIPDevice(Device):
         self._graphs = {}            # ForNode id -> ([graph per staging slot], feeders)
         self._iteration = {}         # ForNode id -> iterations replayed so far
         self._parity = 0
-        self._schedules = {}         # Proc id -> [("launch", fn) | ("cmd", cmd)]
+        self._schedules = {}         # Proc id -> one-lane items (captured into graphs)
+        self._lane_schedules = {}    # Proc id -> items over self.lanes lanes (uncaptured runs)
         self._capturing = False
         self.stats = {"kernels": 0, "unique_sources": 0, "multipass_cmds": 0, "launches_per_iter": 0}
 
@@ -203,17 +204,24 @@ class HIPDevice(Device):
             self.stats["kernels"] += len(ps)
             self.funcs[pid] = launches[0] if len(launches) == 1 else (lambda ls=launches: [f() for f in ls])
         self.ctx.lanes_reserve(self.lanes, self._events)
-        for pid_proc, items in sched.items():
+        launchers = {}
+
+        def bind(items):
             out = []
             for item in items:
                 if item[0] in ("cmd", "record", "wait"):
                     out.append(item)
                     continue
                 _, plan, row, count, lane = item
-                grid = (plan.grid[0], plan.grid[1], count)
-                go = self.ctx.launcher_on(funcs[plan.name], grid, plan.block, plan.shared, [tbase + row])
-                out.append(("launch", go, lane))
-            self._schedules[pid_proc] = out
+                if row not in launchers:
+                    grid = (plan.grid[0], plan.grid[1], count)
+                    launchers[row] = self.ctx.launcher_on(funcs[plan.name], grid, plan.block,
+                                                          plan.shared, [tbase + row])
+                out.append(("launch", launchers[row], lane))
+            return out
+        for pid_proc, (items, lane_items) in sched.items():
+            self._schedules[pid_proc] = bind(items)
+            self._lane_schedules[pid_proc] = bind(lane_items)
         self._pending = []
 
     def _arg_values(self, plan, pid):
@@ -236,7 +244,8 @@ class HIPDevice(Device):
         out = {}
 
         def visit(p):
-            items = []
+            items = []          # one lane
+            lane_items = []     # self.lanes lanes
             stretch = []
 
             def flush():
@@ -257,29 +266,39 @@ class HIPDevice(Device):
                 key = (lambda L: (L.plan.name, L.plan.grid, L.plan.block, L.plan.shared)) \
                     if self.group_launches else (lambda L: None)
                 groups, deps = schedule_dag([(L, L.reads, L.writes) for L in launches], key)
+                rows, plans_of = [], []
+                for group in groups:
+                    members = [launches[i] for i in group]
+                    plans_of.append((members[0].plan, len(members)))
+                    rows.append(add_rows([self._arg_values(m.plan, m.cmd.program_id) for m in members]))
+                # one lane: the groups in order (the form captured into graphs)
+                one = [("launch", plans_of[g][0], rows[g], plans_of[g][1], 0) for g in range(len(groups))]
+                items.extend(one)
+                if self.lanes == 1:
+                    lane_items.extend(one)
+                    stretch.clear()
+                    return
+                # several lanes (uncaptured runs): fork off stream 0, waits
+                # only across lanes, join back at the end of the stretch
                 lane_of, waits = assign_lanes(deps, self.lanes)
-                # fork the lanes this stretch uses off stream 0, join them back at its end
                 used = sorted(set(lane_of) - {0})
                 if used:
                     fork = self._new_event()
-                    items.append(("record", 0, fork))
-                    items.extend(("wait", lane, fork) for lane in used)
+                    lane_items.append(("record", 0, fork))
+                    lane_items.extend(("wait", lane, fork) for lane in used)
                 recorded = {}
                 needed = {d for w in waits for d in w}
-                for g, group in enumerate(groups):
+                for g in range(len(groups)):
                     for d in waits[g]:
-                        items.append(("wait", lane_of[g], recorded[d]))
-                    members = [launches[i] for i in group]
-                    plan = members[0].plan
-                    row = add_rows([self._arg_values(m.plan, m.cmd.program_id) for m in members])
-                    items.append(("launch", plan, row, len(members), lane_of[g]))
+                        lane_items.append(("wait", lane_of[g], recorded[d]))
+                    lane_items.append(("launch", plans_of[g][0], rows[g], plans_of[g][1], lane_of[g]))
                     if g in needed:
                         recorded[g] = self._new_event()
-                        items.append(("record", lane_of[g], recorded[g]))
+                        lane_items.append(("record", lane_of[g], recorded[g]))
                 for lane in used:
                     join = self._new_event()
-                    items.append(("record", lane, join))
-                    items.append(("wait", 0, join))
+                    lane_items.append(("record", lane, join))
+                    lane_items.append(("wait", 0, join))
                 stretch.clear()
 
             for cmd in p.procedure:
@@ -288,12 +307,13 @@ class HIPDevice(Device):
                 if isinstance(cmd, (Feeder, Receiver, ForNode)):
                     flush()
                     items.append(("cmd", cmd))
+                    lane_items.append(("cmd", cmd))
                     if isinstance(cmd, ForNode):
                         visit(cmd.get_proc())
                     continue
                 stretch.append(cmd)
             flush()
-            out[p.id] = items
+            out[p.id] = (items, lane_items)
 
         visit(proc)
         return out
@@ -359,7 +379,9 @@ class HIPDevice(Device):
 
     def _run_scheduled(self, proc):
         ctx = self.ctx
-        for item in self._schedules[proc.id]:
+        items = self._schedules[proc.id] if (self._capturing or self.lanes == 1) \
+            else self._lane_schedules[proc.id]
+        for item in items:
             kind = item[0]
             if kind == "launch":
                 item[1](item[2])
@@ -443,7 +465,8 @@ class HIPDevice(Device):
         for loop in self.loops(proc):
             items = self._schedules[loop.get_proc().id]
             self.stats["launches_per_iter"] = sum(1 for it in items if it[0] == "launch")
-            self.stats["lanes_used"] = len({it[2] for it in items if it[0] == "launch"})
+            lane_items = self._lane_schedules[loop.get_proc().id]
+            self.stats["lanes_used"] = len({it[2] for it in lane_items if it[0] == "launch"})
 
     def execute(self, proc):
         self.prepare(proc)

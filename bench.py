@@ -145,7 +145,7 @@ def micro_elw(reps, copies=2):
     return {"kernel": name, "ms": ms, "bytes": nbytes, "gbs": nbytes / ms / 1e6}
 
 
-def transformer_steps(config, steps, warmup, eager=False):
+def transformer_steps(config, steps, warmup, eager=False, lanes=1):
     import ad_amd as ad
     from ad_amd import workloads
     from ad_amd.device.hip import HIPDevice
@@ -158,7 +158,7 @@ def transformer_steps(config, steps, warmup, eager=False):
     t1 = time.perf_counter()
     step_flops = workloads.dotprod_flops(proc)
     log(f"{config}: traced + compiled in {t1 - t0:.1f} s; {step_flops / 1e12:.3f} TFLOP of DotProd per step")
-    dev = HIPDevice(use_graphs=not eager)
+    dev = HIPDevice(use_graphs=not eager, lanes=lanes)
     dev.prepare(proc)
     t2 = time.perf_counter()
     log(f"{config}: device init + JIT in {t2 - t1:.1f} s; {dev.stats}")
@@ -234,6 +234,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-micro", action="store_true", help="skip the single-command benchmarks")
+    ap.add_argument("--lanes", type=int, default=1,
+                    help="streams for independent launch groups in eager runs (graphs use one)")
     ap.add_argument("--micro-only", action="store_true",
                     help="run only the single-command benchmarks (for counter passes)")
     ap.add_argument("--eager", action="store_true",
@@ -268,7 +270,7 @@ def main():
     if args.micro_only:
         print(json.dumps({"microbench": micro or None}), flush=True)
         return
-    tr = transformer_steps(args.config, args.steps, args.warmup, eager=args.eager)
+    tr = transformer_steps(args.config, args.steps, args.warmup, eager=args.eager, lanes=args.lanes)
     value = args.steps / tr["wall_s"]
     ms_per_step = tr["wall_s"] * 1e3 / args.steps
     log(f"{args.config}: {ms_per_step:.2f} ms/step wall, {tr['event_ms'] / args.steps:.2f} ms/step "

@@ -283,7 +283,7 @@ def test_combine_passes_follow_a_partial_store():
                 combines += 1
                 prev = plans[i - 1]
                 assert prev.family in ("dotprod", "reduce")
-                assert re.search(r"\] = _v(alue)?;", prev.source), prev.source[-600:]
+                assert re.search(r"[\])] = _v(alue)?;", prev.source), prev.source[-600:]
                 slot = [a for a in p.args if a[0] == "scratch"]
                 assert any(a in prev.args for a in slot)
     assert combines > 0

@@ -146,6 +146,15 @@ def test_batched_transformer_parity(hip):
     assert_params_close(a, b)
 
 
+def test_eager_lanes_parity(hip):
+    """Uncaptured run with launch groups spread over four streams (each
+    cross-stream dependency an event wait) against the oracle."""
+    from ad_amd import workloads
+    a, b = run_both(lambda: workloads.transformer(layers=2, d_model=32, heads=4, ff=64, seq=8, batch=2,
+                                                  steps=3), lambda: hip(use_graphs=False, lanes=4))
+    assert_params_close(a, b)
+
+
 def test_layernorm_wide_parity(hip):
     """LayerNorm fwd+bwd at 64 x 1024 (row reductions of 1024 and column
     reductions of 64) for 2 SGD steps on gamma/beta."""
