@@ -20,6 +20,7 @@ constexpr size_t kStageSlotBytes = 8u << 20;   // pinned staging: 8 slots x 8 Mi
 constexpr int kStageSlots = 8;
 constexpr int kEventSlots = 64;
 constexpr int kTags = 4;                        // transfer-stream staging sets
+constexpr int kFetchSets = 2;                   // transfer-stream device->host sets
 
 thread_local std::string g_tls_error;
 
@@ -54,6 +55,15 @@ struct adhip_ctx {
     hipEvent_t released = nullptr; // on stream: the set's device data is consumed
     bool copied_pending = false, released_pending = false, open = false;
   } tags[kTags];
+  // device -> host copies on the transfer stream into pinned memory,
+  // started after the compute stream's work so far
+  struct Fetch {
+    char* host = nullptr;          // pinned
+    size_t cap = 0, used = 0;
+    hipEvent_t ready = nullptr;    // on stream: the data to copy is complete
+    hipEvent_t done = nullptr;     // on xfer: the set's copies are done
+    bool open = false, pending = false;
+  } fetches[kFetchSets];
   // extra compute streams and an event pool for launch graphs with
   // parallel branches (stream 0 is `stream`)
   std::vector<hipStream_t> lanes;
@@ -138,6 +148,11 @@ void adhip_destroy(adhip_ctx* ctx) {
     if (t.copied) hipEventDestroy(t.copied);
     if (t.released) hipEventDestroy(t.released);
     if (t.host) hipHostFree(t.host);
+  }
+  for (auto& f : ctx->fetches) {
+    if (f.ready) hipEventDestroy(f.ready);
+    if (f.done) hipEventDestroy(f.done);
+    if (f.host) hipHostFree(f.host);
   }
   if (ctx->xfer) hipStreamDestroy(ctx->xfer);
   for (auto st : ctx->lanes) {
@@ -269,6 +284,73 @@ int adhip_stage_release(adhip_ctx* ctx, int tag) {
   if (!t.released) return fail(ctx, ADHIP_E_STATE, "staging set %d never used", tag);
   HIP_TRY(ctx, hipEventRecord(t.released, ctx->stream));
   t.released_pending = true;
+  return 0;
+}
+
+int adhip_fetch_reserve(adhip_ctx* ctx, int set, size_t bytes) {
+  if (!ctx || set < 0 || set >= kFetchSets) return fail(ctx, ADHIP_E_ARG, "bad fetch set %d", set);
+  auto& f = ctx->fetches[set];
+  if (f.open || f.pending) return fail(ctx, ADHIP_E_STATE, "fetch set %d in use", set);
+  HIP_TRY(ctx, hipSetDevice(ctx->device));
+  if (!ctx->xfer) HIP_TRY(ctx, hipStreamCreateWithFlags(&ctx->xfer, hipStreamNonBlocking));
+  if (!f.ready) HIP_TRY(ctx, hipEventCreateWithFlags(&f.ready, hipEventDisableTiming));
+  if (!f.done) HIP_TRY(ctx, hipEventCreateWithFlags(&f.done, hipEventDisableTiming));
+  if (bytes > f.cap) {
+    if (f.host) HIP_TRY(ctx, hipHostFree(f.host));
+    f.host = nullptr;
+    f.cap = 0;
+    HIP_TRY(ctx, hipHostMalloc((void**)&f.host, bytes, hipHostMallocDefault));
+    f.cap = bytes;
+  }
+  return 0;
+}
+
+int adhip_fetch_begin(adhip_ctx* ctx, int set) {
+  if (!ctx || set < 0 || set >= kFetchSets) return fail(ctx, ADHIP_E_ARG, "bad fetch set %d", set);
+  if (ctx->capturing) return fail(ctx, ADHIP_E_STATE, "fetch during graph capture");
+  auto& f = ctx->fetches[set];
+  if (!f.ready) return fail(ctx, ADHIP_E_STATE, "fetch set %d not reserved", set);
+  if (f.open || f.pending) return fail(ctx, ADHIP_E_STATE, "fetch set %d not taken yet", set);
+  HIP_TRY(ctx, hipEventRecord(f.ready, ctx->stream));
+  HIP_TRY(ctx, hipStreamWaitEvent(ctx->xfer, f.ready, 0));
+  f.used = 0;
+  f.open = true;
+  return 0;
+}
+
+int adhip_fetch_copy(adhip_ctx* ctx, int set, uint64_t src_off, size_t bytes, size_t* host_off) {
+  if (!ctx || set < 0 || set >= kFetchSets || !host_off) return fail(ctx, ADHIP_E_ARG, "bad argument");
+  auto& f = ctx->fetches[set];
+  if (!f.open) return fail(ctx, ADHIP_E_STATE, "fetch set %d not open", set);
+  if (int r = check_range(ctx, src_off, bytes)) return r;
+  const size_t need = f.used + ((bytes + 255) & ~size_t(255));
+  if (need > f.cap) return fail(ctx, ADHIP_E_ARG, "fetch set %d: %zu bytes reserved, %zu needed", set, f.cap, need);
+  if (bytes) HIP_TRY(ctx, hipMemcpyAsync(f.host + f.used, ctx->arena + src_off, bytes, hipMemcpyDeviceToHost, ctx->xfer));
+  *host_off = f.used;
+  f.used = need;
+  return 0;
+}
+
+int adhip_fetch_end(adhip_ctx* ctx, int set) {
+  if (!ctx || set < 0 || set >= kFetchSets) return fail(ctx, ADHIP_E_ARG, "bad fetch set %d", set);
+  auto& f = ctx->fetches[set];
+  if (!f.open) return fail(ctx, ADHIP_E_STATE, "fetch set %d not open", set);
+  HIP_TRY(ctx, hipEventRecord(f.done, ctx->xfer));
+  f.open = false;
+  f.pending = true;
+  return 0;
+}
+
+int adhip_fetch_take(adhip_ctx* ctx, int set, size_t host_off, void* dst, size_t bytes) {
+  if (!ctx || set < 0 || set >= kFetchSets || (!dst && bytes)) return fail(ctx, ADHIP_E_ARG, "bad argument");
+  auto& f = ctx->fetches[set];
+  if (f.open) return fail(ctx, ADHIP_E_STATE, "fetch set %d still open", set);
+  if (host_off > f.used || bytes > f.used - host_off) return fail(ctx, ADHIP_E_ARG, "fetch set %d: range out of bounds", set);
+  if (f.pending) {
+    HIP_TRY(ctx, hipEventSynchronize(f.done));
+    f.pending = false;
+  }
+  if (bytes) std::memcpy(dst, f.host + host_off, bytes);
   return 0;
 }
 

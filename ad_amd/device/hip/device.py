@@ -16,10 +16,14 @@ replays loop bodies, ``execute`` runs both passes.  Differences by design:
   launches of one kernel merged into one launch; the groups can be spread
   over several streams with event edges only where they touch overlapping
   memory (``lanes``; one stream by default, see ``__init__``);
-* a loop body without Receivers is captured once as a HIP graph and the
+* a loop body without nested loops is captured once as a HIP graph and the
   graph is replayed ``len(r)`` times; a Feeder inside it copies from one of
   two staging slots, which the host refills on a transfer stream while the
-  previous iteration computes (two graphs, one per slot);
+  previous iteration computes (two graphs, one per slot); a Receiver inside
+  it copies its data into one of two snapshot slots, which the transfer
+  stream brings to pinned host memory after the iteration, and its
+  callback runs before the next iteration is launched (``receiver_lag``
+  0) or one iteration later (1);
 * a Feeder writes at its arena offset (the reference OpenCL backend writes
   at offset 0, cl_helper.py:316,326 -- see ``oracle``);
 * after the run, every Tensor's host array is refreshed from the device, as
@@ -67,8 +71,14 @@ class _Launch:
 
 class HIPDevice(Device):
     def __init__(self, device_index: int = 0, use_graphs: bool = True, jit_threads: int = None,
-                 group_launches: bool = True, lanes: int = 1):
+                 group_launches: bool = True, lanes: int = 1, receiver_lag: int = 0):
         super().__init__()
+        # Receivers inside a replayed loop: their callbacks run this many
+        # iterations after the iteration that produced the data (0: before
+        # the next iteration starts, the reference's order; 1: the next
+        # iteration computes meanwhile, and its Feeders are called first)
+        assert receiver_lag in (0, 1), "receiver_lag must be 0 or 1"
+        self.receiver_lag = receiver_lag
         self.kernels = {}            # program_id -> [KernelPlan]
         self.funcs = {}              # program_id -> launch callable (ungrouped)
         self.buffers = {}            # buffer id -> arena byte offset
@@ -88,7 +98,8 @@ class HIPDevice(Device):
         self._contents = {}
         self._pending = []
         self._feeder_slots = {}      # feeder id -> staging byte offset
-        self._graphs = {}            # ForNode id -> ([graph per staging slot], feeders)
+        self._recv_slots = {}        # in-loop receiver id -> (slot byte offset per parity, bytes)
+        self._graphs = {}            # ForNode id -> ([graph per slot parity], feeders, receivers)
         self._iteration = {}         # ForNode id -> iterations replayed so far
         self._parity = 0
         self._schedules = {}         # Proc id -> one-lane items (captured into graphs)
@@ -142,6 +153,21 @@ class HIPDevice(Device):
             size = _align(self._feeder_size.get(fid, 0) * 4)
             self._feeder_slots[fid] = (off, off + size)
             off += 2 * size
+        # two snapshot slots per Receiver in a capturable loop body: the graph
+        # copies the Receiver's data there; the transfer stream fetches it
+        fetch_bytes = [0]
+        for loop in self._all_loops(proc):
+            body = loop.get_proc()
+            if not self._capturable(body):
+                continue
+            per_loop = 0
+            for c in body.procedure:
+                if isinstance(c, Receiver):
+                    size = sum(_align(4 * prod(shape)) for shape in c.shapes)
+                    self._recv_slots[c.id] = ((off, off + size), size)
+                    off += 2 * size
+                    per_loop += size
+            fetch_bytes[0] = max(fetch_bytes[0], per_loop)
         # kernel plans and the ranges each command touches; commands that need
         # scratch get consecutive slots of a ring, so neighbouring commands do
         # not share scratch and can run in one launch
@@ -185,6 +211,9 @@ class HIPDevice(Device):
         self.table_off = off
         off += _align(max(table_bytes[0], 8))
         self.ctx.reserve(max(off, ALIGN))
+        if fetch_bytes[0]:
+            for fset in (0, 1):
+                self.ctx.fetch_reserve(fset, fetch_bytes[0])
         for bid, content in self._contents.items():
             assert content.dtype == np.float32, "Content is not np.float32"
             self.ctx.write(self.buffers[bid], np.ascontiguousarray(content))
@@ -359,6 +388,15 @@ class HIPDevice(Device):
             self.ctx.write(self.buffers[cmd.kres.id] + 4 * cmd.kres.offset, arr)
             return
         if isinstance(cmd, Receiver):
+            if self._capturing:
+                # inside a graph: snapshot the data into this iteration's slot
+                dst = self._recv_slots[cmd.id][0][self._parity]
+                for bid, shape, off in zip(cmd.ids, cmd.shapes, cmd.offsets):
+                    n = 4 * prod(shape)
+                    self.ctx.copy(dst, self.buffers[bid] + 4 * off, n)
+                    dst += _align(n)
+                self._graph_receivers.append(cmd)
+                return
             outs = []
             for bid, shape, off in zip(cmd.ids, cmd.shapes, cmd.offsets):
                 out = np.empty(shape, dtype=np.float32)
@@ -375,7 +413,26 @@ class HIPDevice(Device):
         return np.ascontiguousarray(arr, dtype=np.float32)
 
     def _capturable(self, proc):
-        return not any(isinstance(c, (Receiver, ForNode)) for c in proc.procedure)
+        """A loop body replays as a graph unless it holds a loop, or a Feeder
+        after a Receiver (its function would run before the Receiver's
+        callback of the same iteration)."""
+        seen_receiver = False
+        for c in proc.procedure:
+            if isinstance(c, ForNode):
+                return False
+            if isinstance(c, Receiver):
+                seen_receiver = True
+            elif isinstance(c, Feeder) and seen_receiver:
+                return False
+        return True
+
+    def _all_loops(self, proc):
+        out = []
+        for c in proc.procedure:
+            if isinstance(c, ForNode):
+                out.append(c)
+                out.extend(self._all_loops(c.get_proc()))
+        return out
 
     def _run_scheduled(self, proc):
         ctx = self.ctx
@@ -409,31 +466,61 @@ class HIPDevice(Device):
             for parity in (0, 1):            # one graph per staging slot
                 self._capturing, self._parity = True, parity
                 self._graph_feeders = []
+                self._graph_receivers = []
                 self.ctx.graph_begin()
                 try:
                     self._run_scheduled(inner)
                 finally:
                     self._capturing = False
                     graphs.append(self.ctx.graph_end())
-                if not self._graph_feeders:
-                    break                    # no Feeder: one graph serves every iteration
-            self._graphs[cmd.id] = (graphs, self._graph_feeders)
+                if not self._graph_feeders and not self._graph_receivers:
+                    break                    # one graph serves every iteration
+            self._graphs[cmd.id] = (graphs, self._graph_feeders, self._graph_receivers)
             self._iteration[cmd.id] = 0
-        graphs, feeders = self._graphs[cmd.id]
+        graphs, feeders, receivers = self._graphs[cmd.id]
+        waiting = []                         # fetched iterations whose callbacks are due
         for _ in range(reps):
+            parity = self._iteration[cmd.id] & 1
             if feeders:
                 # this iteration's inputs go up on the transfer stream while the
                 # previous iteration computes; the graph waits for them
-                parity = self._iteration[cmd.id] & 1
                 self.ctx.stage_begin(parity)
                 for f in feeders:
                     self.ctx.stage_write(parity, self._feeder_slots[f.id][parity], self._feeder_value(f))
                 self.ctx.stage_end(parity)
-                self.ctx.graph_launch(graphs[parity])
+            self.ctx.graph_launch(graphs[parity if len(graphs) > 1 else 0])
+            if feeders:
                 self.ctx.stage_release(parity)
-            else:
-                self.ctx.graph_launch(graphs[0])
+            if receivers:
+                # the snapshots of this iteration come down on the transfer stream
+                self.ctx.fetch_begin(parity)
+                taken = [self._fetch_receiver(r, parity) for r in receivers]
+                self.ctx.fetch_end(parity)
+                waiting.append((parity, taken))
+                if len(waiting) > self.receiver_lag:
+                    self._deliver(*waiting.pop(0))
             self._iteration[cmd.id] += 1
+        for item in waiting:
+            self._deliver(*item)
+
+    def _fetch_receiver(self, r, parity):
+        src = self._recv_slots[r.id][0][parity]
+        parts = []
+        for shape in r.shapes:
+            n = 4 * prod(shape)
+            parts.append((self.ctx.fetch_copy(parity, src, n), shape))
+            src += _align(n)
+        return r, parts
+
+    def _deliver(self, parity, taken):
+        """Receiver callbacks of one fetched iteration, in body order."""
+        for r, parts in taken:
+            outs = []
+            for host_off, shape in parts:
+                out = np.empty(shape, dtype=np.float32)
+                self.ctx.fetch_take(parity, host_off, out)
+                outs.append(out)
+            r.func(*outs)
 
     def _run_proc(self, proc, func, init=False):
         """The reference's command walk (device.py:114-124), used for the init
@@ -496,7 +583,7 @@ class HIPDevice(Device):
             content.reshape(-1)[:] = out
 
     def close(self):
-        for graphs, _ in self._graphs.values():
+        for graphs, _, _ in self._graphs.values():
             for g in graphs:
                 self.ctx.graph_destroy(g)
         self._graphs = {}

@@ -18,6 +18,7 @@ _lock = threading.Lock()
 EXPORTS = [
     "adhip_create", "adhip_destroy", "adhip_last_error", "adhip_device_info", "adhip_arena_reserve",
     "adhip_write", "adhip_stage_begin", "adhip_stage_write", "adhip_stage_end", "adhip_stage_release",
+    "adhip_fetch_reserve", "adhip_fetch_begin", "adhip_fetch_copy", "adhip_fetch_end", "adhip_fetch_take",
     "adhip_read", "adhip_copy", "adhip_compile", "adhip_free", "adhip_module_load",
     "adhip_module_function", "adhip_launch", "adhip_graph_begin", "adhip_graph_end",
     "adhip_graph_launch", "adhip_graph_destroy", "adhip_sync", "adhip_event_record",
@@ -51,6 +52,11 @@ def load_library(path=LIB_PATH):
             "adhip_stage_write": (i32, [vp, i32, u64, vp, sz]),
             "adhip_stage_end": (i32, [vp, i32]),
             "adhip_stage_release": (i32, [vp, i32]),
+            "adhip_fetch_reserve": (i32, [vp, i32, sz]),
+            "adhip_fetch_begin": (i32, [vp, i32]),
+            "adhip_fetch_copy": (i32, [vp, i32, u64, sz, ctypes.POINTER(ctypes.c_size_t)]),
+            "adhip_fetch_end": (i32, [vp, i32]),
+            "adhip_fetch_take": (i32, [vp, i32, sz, vp, sz]),
             "adhip_read": (i32, [vp, u64, vp, sz]),
             "adhip_copy": (i32, [vp, u64, u64, sz]),
             "adhip_compile": (i32, [c.c_char_p, c.c_char_p, c.POINTER(vp), c.POINTER(sz), c.c_char_p, sz]),
@@ -149,6 +155,25 @@ class Context:
 
     def stage_release(self, tag: int):
         self.check(self.lib.adhip_stage_release(self.h, tag), "adhip_stage_release")
+
+    def fetch_reserve(self, fset: int, nbytes: int):
+        self.check(self.lib.adhip_fetch_reserve(self.h, fset, nbytes), "adhip_fetch_reserve")
+
+    def fetch_begin(self, fset: int):
+        self.check(self.lib.adhip_fetch_begin(self.h, fset), "adhip_fetch_begin")
+
+    def fetch_copy(self, fset: int, byte_off: int, nbytes: int) -> int:
+        host_off = ctypes.c_size_t()
+        self.check(self.lib.adhip_fetch_copy(self.h, fset, byte_off, nbytes, ctypes.byref(host_off)),
+                   "adhip_fetch_copy")
+        return host_off.value
+
+    def fetch_end(self, fset: int):
+        self.check(self.lib.adhip_fetch_end(self.h, fset), "adhip_fetch_end")
+
+    def fetch_take(self, fset: int, host_off: int, arr):
+        self.check(self.lib.adhip_fetch_take(self.h, fset, host_off, arr.ctypes.data, arr.nbytes),
+                   "adhip_fetch_take")
 
     def read(self, byte_off: int, arr):
         self.check(self.lib.adhip_read(self.h, byte_off, arr.ctypes.data, arr.nbytes), "adhip_read")

@@ -15,6 +15,9 @@
 * ``microbench``: the same figures for the Reduce+Elw (``sum(-1)*c`` over
   [8192,4096]) and ElwFuse (6 ops over 64M floats) commands, HBM-bound, with
   inputs rotated across copies larger than the 256 MB last-level cache.
+* ``other_configs``: C1 (the MLP of examples/linear.py, a Feeder upload per
+  step), C3 (LayerNorm fwd+bwd at [16384,1024], GB/s over its 5-pass HBM
+  floor) and C4 (1-layer transformer) at full size, graph-replayed.
 * ``cpu_baseline``: the CPU restatement of the reference OpenCL backend
   (``oracle``, one OpenMP iteration per work-item, sequential k-loops) timed
   on this host on a bounded sample of the same workload (the step's FFN
@@ -181,6 +184,65 @@ def transformer_steps(config, steps, warmup, eager=False, lanes=1):
             "compile_s": t1 - t0, "init_s": t2 - t1, "launches_per_step": launches}
 
 
+def loop_rate(build, steps, warmup):
+    """Per-iteration device time of the one ``ir_for`` a builder traces,
+    replayed as a HIP graph (a Feeder's host function and upload included)."""
+    import ad_amd as ad
+    from ad_amd.device.hip import HIPDevice
+    ad.reset()
+    build()
+    proc = ad.compile_proc()
+    dev = HIPDevice()
+    dev.prepare(proc)
+    loop = dev.loops(proc)
+    assert len(loop) == 1
+    loop = loop[0]
+    dev.replay(loop, max(1, warmup))
+    dev.ctx.sync()
+    t0 = time.perf_counter()
+    dev.ctx.event(0)
+    dev.replay(loop, steps)
+    dev.ctx.event(1)
+    dev.ctx.sync()
+    wall = time.perf_counter() - t0
+    ev_ms = dev.ctx.elapsed_ms(0, 1)
+    launches = dev.stats["launches_per_iter"]
+    dev.close()
+    return {"ms": max(wall * 1e3, ev_ms) / steps, "launches": launches}
+
+
+# bytes of the 5-pass floor of one LayerNorm fwd+bwd iteration at [16384, 1024]:
+# five passes over a 64 MiB matrix
+C3_FLOOR_BYTES = 5 * 4 * 16384 * 1024
+
+
+def other_configs():
+    """C1 (MLP, Feeder per step), C3 (LayerNorm fwd+bwd) and C4 (1-layer
+    transformer) at their full sizes."""
+    from ad_amd import workloads
+    out = {}
+    c1 = loop_rate(lambda: workloads.mlp(steps=1, receive=False), 1000, 50)
+    out["c1_mlp"] = {"workload": "Linear(255,255)-Sigmoid-Linear(255,255), [2,255] Feeder per step, SGD",
+                     "us_per_step": round(c1["ms"] * 1e3, 2), "steps_per_s": round(1e3 / c1["ms"], 1),
+                     "launches_per_step": c1["launches"]}
+    log(f"c1: {c1['ms'] * 1e3:.1f} us/step, {c1['launches']} launches/step")
+    c3 = loop_rate(lambda: workloads.layernorm_train(rows=16384, cols=1024, steps=1, receive=False), 50, 3)
+    gbs = C3_FLOOR_BYTES / c3["ms"] / 1e6
+    out["c3_layernorm"] = {"workload": "LayerNorm fwd+bwd [16384,1024] + SGD on gamma/beta",
+                           "ms_per_iter": round(c3["ms"], 4), "floor_bytes": C3_FLOOR_BYTES,
+                           "floor_gbs": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4),
+                           "launches_per_iter": c3["launches"]}
+    log(f"c3: {c3['ms'] * 1e3:.1f} us/iter, {gbs:.0f} GB/s over the 5-pass floor")
+    c4 = transformer_steps("c4", 20, 3)
+    ms = c4["event_ms"] / 20
+    out["c4_transformer"] = {"workload": "1-layer encoder d_model 512, 8 heads, FFN 2048, seq 256, batch 16",
+                             "steps_per_s": round(1e3 / ms, 2), "ms_per_step": round(ms, 3),
+                             "step_dotprod_tflops": round(c4["step_flops"] / (ms * 1e9), 2),
+                             "launches_per_step": c4["launches_per_step"]}
+    log(f"c4: {ms:.2f} ms/step, {1e3 / ms:.1f} steps/s")
+    return out
+
+
 def cpu_baseline(config, step_flops, seconds):
     """The oracle's work-item kernel for the step's FFN-expand DotProd+Elw
     (``relu(X @ W1 + b1)``, K = d_model, N = ffn) on a row slice of X,
@@ -234,6 +296,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-micro", action="store_true", help="skip the single-command benchmarks")
+    ap.add_argument("--no-configs", action="store_true", help="skip the C1/C3/C4 measurements")
     ap.add_argument("--lanes", type=int, default=1,
                     help="streams for independent launch groups in eager runs (graphs use one)")
     ap.add_argument("--micro-only", action="store_true",
@@ -276,6 +339,8 @@ def main():
     log(f"{args.config}: {ms_per_step:.2f} ms/step wall, {tr['event_ms'] / args.steps:.2f} ms/step "
         f"events, {value:.3f} steps/s, {tr['launches_per_step']} launches/step")
 
+    others = None if args.no_configs else other_configs()
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(args.config, tr["step_flops"], args.cpu_seconds)
@@ -306,6 +371,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "microbench": micro or None,
+        "other_configs": others,
     }
     print(json.dumps(out), flush=True)
 

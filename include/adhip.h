@@ -73,6 +73,22 @@ int  adhip_stage_write(adhip_ctx* ctx, int tag, uint64_t dst_off, const void* ho
 int  adhip_stage_end(adhip_ctx* ctx, int tag);
 int  adhip_stage_release(adhip_ctx* ctx, int tag);
 
+/* Device -> host copies on the transfer stream into pinned memory, for
+ * Receivers inside a replayed loop.  A fetch set (0..1) is reserved once
+ * (pinned capacity), then per round: begin (the copies start after all
+ * work queued on the compute stream so far), copy (returns where in the
+ * set's pinned memory the bytes will land), end, and take (waits for the
+ * set's copies on its first call, then copies into the caller's buffer).
+ * A set must be taken before it begins again.  Replaces the blocking
+ * clEnqueueReadBuffer of read_buffers (cl_helper.py:262-302) and the
+ * unfinished read_buffers_async (cl_helper.py:176-260) for in-loop
+ * Receivers. */
+int  adhip_fetch_reserve(adhip_ctx* ctx, int set, size_t bytes);
+int  adhip_fetch_begin(adhip_ctx* ctx, int set);
+int  adhip_fetch_copy(adhip_ctx* ctx, int set, uint64_t src_off, size_t bytes, size_t* host_off);
+int  adhip_fetch_end(adhip_ctx* ctx, int set);
+int  adhip_fetch_take(adhip_ctx* ctx, int set, size_t host_off, void* dst, size_t bytes);
+
 /* Stream-ordered device -> device copy inside the arena (capturable). */
 int  adhip_copy(adhip_ctx* ctx, uint64_t dst_off, uint64_t src_off, size_t bytes);
 

@@ -31,6 +31,28 @@ def mlp(steps=3, din=255, dh=255, dout=255, rows=2, fill=0.2):
     return out
 
 
+def mlp_logged(steps=5, din=16, dh=32, dout=8, rows=4):
+    """A small MLP trained in a loop whose body also receives the network's
+    output every iteration (per-step logging); returns the outputs in
+    callback order and the final parameters."""
+    net = Sequential(Linear(din, dh), Sigmoid(), Linear(dh, dout))
+    set_uniform(net.parameters(), 0)
+    opt = SGD(net.parameters(), lr=0.5)
+    x = np.random.default_rng(1).uniform(-1, 1, (rows, din)).astype(np.float32)
+    out = {"log": []}
+
+    def body():
+        opt.zero_grad()
+        val = ad.Feeder(lambda: x, shape=[rows, din])
+        y = net(val)
+        y.backward()
+        opt.step()
+        Receiver(lambda v: out["log"].append(v.copy()), [y])
+    ad.ir_for(range(steps), body)
+    Receiver(lambda *a: out.setdefault("params", [v.copy() for v in a]), opt.parameters)
+    return out
+
+
 def layernorm_step(rows=8, cols=16, steps=2):
     """LayerNorm fwd+bwd with SGD on gamma/beta; loss = sum(LN(x) * dy)."""
     rng = np.random.default_rng(1)

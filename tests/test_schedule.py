@@ -162,3 +162,27 @@ def test_dag_lanes_order_every_conflict(seed):
             if _conflict(launches[i], launches[j]):
                 gi, gj = group_of[i], group_of[j]
                 assert gi != gj and gi in before[gj], (i, j)
+
+
+def test_loop_bodies_with_receivers_are_capturable():
+    """A loop body with Receivers replays as a graph (their data is
+    snapshotted and fetched); one with a Feeder after a Receiver, or a nested
+    loop, runs command by command."""
+    from types import SimpleNamespace
+
+    import numpy as np
+
+    import ad_amd as ad
+    from ad_amd.device.hip.device import HIPDevice
+    from ad_amd.graph import Feeder, ForNode, Receiver, Tensor
+    ad.reset()
+    t = Tensor(np.zeros((2, 2), dtype=np.float32))
+    f = Feeder(lambda: np.zeros((2, 2), np.float32), shape=[2, 2])
+    r = Receiver(lambda v: None, [t])
+    ok = HIPDevice._capturable
+    assert ok(None, SimpleNamespace(procedure=[f, r]))
+    assert ok(None, SimpleNamespace(procedure=[r, r]))
+    assert not ok(None, SimpleNamespace(procedure=[r, f]))
+    loop = ForNode.__new__(ForNode)
+    assert not ok(None, SimpleNamespace(procedure=[f, loop]))
+    ad.reset()
