@@ -45,19 +45,24 @@ struct EP4 { float* p0; static constexpr bool kVec4 = true; static constexpr int
   __device__ void load4(unsigned x, unsigned y, float4* l) const { l[0] = *reinterpret_cast<const float4*>(p0 + x * 64u + y); }
   __device__ void vec(float4 v, unsigned x, unsigned y, int c, const float4* l) const {
     *reinterpret_cast<float4*>(p0 + (c * 64u + x) * 64u + y) = make_float4(v.x + l[0].x, v.y + l[0].y, v.z + l[0].z, v.w + l[0].w); } };
-struct LD { static constexpr bool kVec = true; float* p0;
+struct LD { static constexpr bool kVec = true; static constexpr bool kVecX = false; float* p0;
   __device__ float at(unsigned x, unsigned y) const { return p0[x * 64u + y]; }
   __device__ float4 at4(unsigned x, unsigned y) const { return *reinterpret_cast<const float4*>(p0 + x * 64u + y); }
   __device__ bool inc(unsigned) const { return true; } };
+struct LDX { static constexpr bool kVec = false; static constexpr bool kVecX = true; float* p0;
+  __device__ float at(unsigned x, unsigned y) const { return p0[y * 64u + x]; }
+  __device__ float4 at4(unsigned x, unsigned y) const { return *reinterpret_cast<const float4*>(p0 + y * 64u + x); }
+  __device__ bool inc(unsigned) const { return true; } };
 struct EPR { float* p0; __device__ void operator()(float v, unsigned x, int c) const { p0[c * 64u + x] = v; } };
-extern "C" __global__ void __launch_bounds__(256) probe_dp(float* a) { adhip::dp_mfma<128, 128, 1>(LA{a}, LB{a}, EPI{a}, 64, 64, 64); }
-extern "C" __global__ void __launch_bounds__(256) probe_dp_narrow(float* a) { adhip::dp_mfma<128, 64, 4>(LA{a}, LB{a}, EPI{a}, 64, 64, 64); }
-extern "C" __global__ void __launch_bounds__(256) probe_dp_small(float* a) { adhip::dp_mfma<64, 64, 2>(LA{a}, LB{a}, EPI{a}, 64, 64, 64); }
-extern "C" __global__ void __launch_bounds__(256) probe_dp_vec(float* a) { adhip::dp_mfma<128, 64, 1>(LA{a}, LB{a}, EP4{a}, 64, 64, 64); }
-extern "C" __global__ void __launch_bounds__(256) probe_dp_vec_small(float* a) { adhip::dp_mfma<64, 64, 4>(LA{a}, LB{a}, EP4{a}, 64, 64, 64); }
+extern "C" __global__ void __launch_bounds__(256) probe_dp(float* a) { adhip::dp_mfma<128, 128, 1, 16>(LA{a}, LB{a}, EPI{a}, 64, 64, 64); }
+extern "C" __global__ void __launch_bounds__(256) probe_dp_narrow(float* a) { adhip::dp_mfma<128, 64, 4, 32>(LA{a}, LB{a}, EPI{a}, 64, 64, 64); }
+extern "C" __global__ void __launch_bounds__(256) probe_dp_small(float* a) { adhip::dp_mfma<64, 64, 2, 16>(LA{a}, LB{a}, EPI{a}, 64, 64, 64); }
+extern "C" __global__ void __launch_bounds__(256) probe_dp_vec(float* a) { adhip::dp_mfma<128, 64, 1, 16>(LA{a}, LB{a}, EP4{a}, 64, 64, 64); }
+extern "C" __global__ void __launch_bounds__(256) probe_dp_vec_small(float* a) { adhip::dp_mfma<64, 64, 4, 64>(LA{a}, LB{a}, EP4{a}, 64, 64, 64); }
 extern "C" __global__ void __launch_bounds__(256) probe_rr(float* a) { adhip::reduce_rows<0>(LD{a}, EPR{a}, 64u, 64u, false); }
 extern "C" __global__ void __launch_bounds__(256) probe_rc(float* a) { adhip::reduce_cols<1, 1>(LD{a}, EPR{a}, 64u, 64u, true); }
 extern "C" __global__ void __launch_bounds__(256) probe_rcs(float* a) { adhip::reduce_cols<0, 8>(LD{a}, EPR{a}, 64u, 64u, false); }
+extern "C" __global__ void __launch_bounds__(256) probe_rcv(float* a) { adhip::reduce_cols<0, 8>(LDX{a}, EPR{a}, 64u, 64u, false); }
 '''
     compile_source(header + probe)
 

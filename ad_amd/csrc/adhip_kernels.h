@@ -9,9 +9,9 @@
 //                    into chunks, epilogue in registers.
 //  * reduce_rows  -- Reduce+Elw, rows contiguous: waves striding over rows,
 //                    float4 or scalar coalesced loads, butterfly over the wave.
-//  * reduce_cols  -- Reduce+Elw, columns contiguous: 64 columns x 4 row groups
-//                    per block, coalesced along the columns, LDS combine,
-//                    optional split of the rows into chunks.
+//  * reduce_cols  -- Reduce+Elw, columns contiguous: 64 or 256 (float4)
+//                    columns x 4 row groups per block, coalesced along the
+//                    columns, LDS combine, optional split of the rows.
 // Elementwise (ElwFuse) kernels are emitted whole by the generator.
 #pragma clang fp contract(off)
 
@@ -31,7 +31,7 @@ __device__ __forceinline__ float rop(float a, float b) {
 // LA::kMode: 0 = contiguous along k, 1 = contiguous along m.
 // LB::kMode: 0 = contiguous along n, 1 = contiguous along k.
 //
-// Block tile BM x BN, K panels of DP_BK staged in two LDS buffers, 4 waves as
+// Block tile BM x BN, K panels of BK staged in two LDS buffers, 4 waves as
 // 2 x 2, each wave (BM/2) x (BN/2) made of 32x32 v_mfma_f32_32x32x2f32 tiles;
 // the next panel is prefetched into registers while the current one is
 // consumed, then stored into the other buffer.
@@ -45,23 +45,24 @@ __device__ __forceinline__ float rop(float a, float b) {
 // epi.load4(row, col, l) fills float4 operand registers for the lane's 4
 // groups, then epi.vec(value4, row, col, chunk, l) runs the statements on 4
 // elements with float4 loads and stores.
-constexpr int DP_BK = 16, DP_PAD = 4, DP_GROUP = 8, DP_CPITCH = 40;
+constexpr int DP_PAD = 4, DP_GROUP = 8, DP_CPITCH = 40;
 
-template <int BM, int BN, int SPLIT, class LA, class LB, class EPI>
+template <int BM, int BN, int SPLIT, int BK, class LA, class LB, class EPI>
 __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& epi, int M, int N, int K) {
   static_assert(BM % 64 == 0 && BN % 64 == 0, "tile must be a multiple of 64");
+  static_assert(BK % 16 == 0, "K panel must be a multiple of 16");
   constexpr int TM = BM / 64, TN = BN / 64;              // 32x32 tiles per wave
-  constexpr int VA = BM * DP_BK / 4 / 256;               // float4 loads per thread
-  constexpr int VB = BN * DP_BK / 4 / 256;
+  constexpr int VA = BM * BK / 4 / 256;               // float4 loads per thread
+  constexpr int VB = BN * BK / 4 / 256;
   static_assert(VA >= 1 && VB >= 1, "tile too small for 256 threads");
   // K panels (two buffers of A and of B) and, after the products, the
   // per-wave 32x32 staging of the vectorised epilogue share one LDS block
-  constexpr int A_FLOATS = 2 * DP_BK * (BM + DP_PAD), B_FLOATS = 2 * DP_BK * (BN + DP_PAD);
+  constexpr int A_FLOATS = 2 * BK * (BM + DP_PAD), B_FLOATS = 2 * BK * (BN + DP_PAD);
   constexpr int C_FLOATS = EPI::kVec4 ? 4 * 32 * DP_CPITCH : 0;
   constexpr int S_FLOATS = A_FLOATS + B_FLOATS > C_FLOATS ? A_FLOATS + B_FLOATS : C_FLOATS;
   __shared__ __attribute__((aligned(16))) float smem[S_FLOATS];
-  float (*As)[DP_BK][BM + DP_PAD] = reinterpret_cast<float (*)[DP_BK][BM + DP_PAD]>(smem);
-  float (*Bs)[DP_BK][BN + DP_PAD] = reinterpret_cast<float (*)[DP_BK][BN + DP_PAD]>(smem + A_FLOATS);
+  float (*As)[BK][BM + DP_PAD] = reinterpret_cast<float (*)[BK][BM + DP_PAD]>(smem);
+  float (*Bs)[BK][BN + DP_PAD] = reinterpret_cast<float (*)[BK][BN + DP_PAD]>(smem + A_FLOATS);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -85,7 +86,7 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
   const int m0 = (SPLIT > 1 ? by % tiles_m : by) * BM, n0 = bx * BN;
   int kbeg = 0, kend = K;
   if constexpr (SPLIT > 1) {
-    const int kc = ((K + SPLIT - 1) / SPLIT + DP_BK - 1) / DP_BK * DP_BK;
+    const int kc = ((K + SPLIT - 1) / SPLIT + BK - 1) / BK * BK;
     kbeg = chunk * kc;
     kend = kbeg + kc < K ? kbeg + kc : K;
   }
@@ -97,7 +98,7 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
     for (int i = 0; i < VA; ++i) {
       const int v = tid + 256 * i;
       if constexpr (LA::kMode == 0) {          // row of 4 consecutive k
-        const int m = m0 + v / (DP_BK / 4), k = k0 + 4 * (v % (DP_BK / 4));
+        const int m = m0 + v / (BK / 4), k = k0 + 4 * (v % (BK / 4));
         if constexpr (LA::kVec) {
           const float4 x = (m < M && k < kend) ? la.at4(m, k) : make_float4(0.f, 0.f, 0.f, 0.f);
           ra[i][0] = x.x; ra[i][1] = x.y; ra[i][2] = x.z; ra[i][3] = x.w;
@@ -122,7 +123,7 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
     for (int i = 0; i < VA; ++i) {
       const int v = tid + 256 * i;
       if constexpr (LA::kMode == 0) {
-        const int m = v / (DP_BK / 4), k = 4 * (v % (DP_BK / 4));
+        const int m = v / (BK / 4), k = 4 * (v % (BK / 4));
 #pragma unroll
         for (int j = 0; j < 4; ++j) As[buf][k + j][m] = ra[i][j];
       } else {
@@ -145,7 +146,7 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
           for (int j = 0; j < 4; ++j) rb[i][j] = (k < kend && n + j < N) ? lb.at(k, n + j) : 0.f;
         }
       } else {                                  // column of 4 consecutive k
-        const int n = n0 + v / (DP_BK / 4), k = k0 + 4 * (v % (DP_BK / 4));
+        const int n = n0 + v / (BK / 4), k = k0 + 4 * (v % (BK / 4));
         if constexpr (LB::kVec) {
           const float4 x = (n < N && k < kend) ? lb.at4(k, n) : make_float4(0.f, 0.f, 0.f, 0.f);
           rb[i][0] = x.x; rb[i][1] = x.y; rb[i][2] = x.z; rb[i][3] = x.w;
@@ -164,7 +165,7 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
         const int k = v / (BN / 4), n = 4 * (v % (BN / 4));
         *reinterpret_cast<float4*>(&Bs[buf][k][n]) = make_float4(rb[i][0], rb[i][1], rb[i][2], rb[i][3]);
       } else {
-        const int n = v / (DP_BK / 4), k = 4 * (v % (DP_BK / 4));
+        const int n = v / (BK / 4), k = 4 * (v % (BK / 4));
 #pragma unroll
         for (int j = 0; j < 4; ++j) Bs[buf][k + j][n] = rb[i][j];
       }
@@ -190,14 +191,14 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
     store_b(0);
     __syncthreads();
     int cur = 0;
-    for (int k0 = kbeg; k0 < kend; k0 += DP_BK) {
-      const bool more = k0 + DP_BK < kend;
+    for (int k0 = kbeg; k0 < kend; k0 += BK) {
+      const bool more = k0 + BK < kend;
       if (more) {
-        load_a(k0 + DP_BK);
-        load_b(k0 + DP_BK);
+        load_a(k0 + BK);
+        load_b(k0 + BK);
       }
 #pragma unroll
-      for (int kk = 0; kk < DP_BK; kk += 2) {
+      for (int kk = 0; kk < BK; kk += 2) {
         float a[TM], b[TN];
 #pragma unroll
         for (int i = 0; i < TM; ++i) a[i] = As[cur][kk + lk][wm * (BM / 2) + i * 32 + lr];
@@ -316,32 +317,69 @@ __device__ __forceinline__ void reduce_rows(const LD& ld, const EPI& epi, unsign
   }
 }
 
-// reduce_cols: 64 columns x 4 row groups per block, coalesced along the
-// columns, LDS combine.  SPLIT > 1 splits the rows into SPLIT chunks
-// (blockIdx.y) whose results go to the epilogue with the chunk index and
-// without the zero padding of MAX (applied once the chunks are combined).
+// reduce_cols: a block covers 64*W columns (W = 4 consecutive columns per
+// lane loaded as one float4 when LD::kVecX, else 1) and 4 row groups, one
+// per wave (group g takes rows g, g+4, ...); a lane keeps 8 rows' loads in
+// flight; the 4 groups combine through LDS.  SPLIT > 1 splits the rows into
+// SPLIT chunks (blockIdx.y) whose results go to the epilogue with the chunk
+// index and without the zero padding of MAX (applied once the chunks are
+// combined).  Every column sums its rows in order within a group.
 template <int OP, int SPLIT, class LD, class EPI>
 __device__ __forceinline__ void reduce_cols(const LD& ld, const EPI& epi, unsigned V, unsigned R,
                                             bool pad_zero) {
-  __shared__ float part[4][64];
+  constexpr int W = LD::kVecX ? 4 : 1;
+  __shared__ float part[4][64 * W];
   const unsigned lane = threadIdx.x & 63, grp = threadIdx.x >> 6;
-  const unsigned col = blockIdx.x * 64 + lane;
+  const unsigned col0 = blockIdx.x * (64 * W) + lane * W;
   unsigned ybeg = 0, yend = R;
   if constexpr (SPLIT > 1) {
     const unsigned rc = (R + SPLIT - 1) / SPLIT;
     ybeg = blockIdx.y * rc;
     yend = ybeg + rc < R ? ybeg + rc : R;
   }
-  float acc = OP == 0 ? 0.f : -__builtin_huge_valf();
-  if (col < V)
-    for (unsigned y = ybeg + grp; y < yend; y += 4)
-      if (ld.inc(y)) acc = rop<OP>(acc, ld.at(col, y));
-  part[grp][lane] = acc;
+  const float id = OP == 0 ? 0.f : -__builtin_huge_valf();
+  float acc[W];
+#pragma unroll
+  for (int w = 0; w < W; ++w) acc[w] = id;
+  if constexpr (W == 4) {
+    // V % 4 == 0: a lane's 4 columns are all in range or all out
+    if (col0 < V) {
+      unsigned y = ybeg + grp;
+      for (; y + 28 < yend; y += 32) {
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = ld.at4(col0, y + 4 * u);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          acc[0] = rop<OP>(acc[0], v[u].x);
+          acc[1] = rop<OP>(acc[1], v[u].y);
+          acc[2] = rop<OP>(acc[2], v[u].z);
+          acc[3] = rop<OP>(acc[3], v[u].w);
+        }
+      }
+      for (; y < yend; y += 4) {
+        const float4 v = ld.at4(col0, y);
+        acc[0] = rop<OP>(acc[0], v.x);
+        acc[1] = rop<OP>(acc[1], v.y);
+        acc[2] = rop<OP>(acc[2], v.z);
+        acc[3] = rop<OP>(acc[3], v.w);
+      }
+    }
+  } else {
+    if (col0 < V)
+      for (unsigned y = ybeg + grp; y < yend; y += 4)
+        if (ld.inc(y)) acc[0] = rop<OP>(acc[0], ld.at(col0, y));
+  }
+#pragma unroll
+  for (int w = 0; w < W; ++w) part[grp][lane * W + w] = acc[w];
   __syncthreads();
-  if (grp == 0 && col < V) {
-    acc = rop<OP>(rop<OP>(rop<OP>(part[0][lane], part[1][lane]), part[2][lane]), part[3][lane]);
-    if (SPLIT == 1 && OP == 1 && pad_zero) acc = fmaxf(acc, 0.f);
-    epi(acc, col, (int)blockIdx.y);
+  for (unsigned t = threadIdx.x; t < 64u * W; t += blockDim.x) {
+    const unsigned col = blockIdx.x * (64 * W) + t;
+    if (col < V) {
+      float a = rop<OP>(rop<OP>(rop<OP>(part[0][t], part[1][t]), part[2][t]), part[3][t]);
+      if (SPLIT == 1 && OP == 1 && pad_zero) a = fmaxf(a, 0.f);
+      epi(a, col, (int)blockIdx.y);
+    }
   }
 }
 

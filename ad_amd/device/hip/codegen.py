@@ -667,21 +667,28 @@ def elementwise_plan(stmts, n, index_kind="global", n_cols=1, flops=0, init_valu
     bound = _expr_bound(stmts, max(n - 1, 0), max(n - 1, 0), max(n_cols - 1, 0))
     ity = _ity(bound)
     setup = _index_setup(index_kind, ity, n_cols)
-    if not _vector_plan(stmts, n, index_kind, n_cols):
+    # combining many partial results for few elements: one element per
+    # thread in 64-thread blocks spreads the partials' loads over more
+    # compute units than a few 256-thread blocks of float4 lanes would
+    many_partials = any(k == "sum" and node[1] >= 16 for k, node in stmts)
+    narrow = many_partials and ceil(n / (4 * BLOCK)) < 64
+    if narrow or not _vector_plan(stmts, n, index_kind, n_cols):
+        block = 64 if narrow else BLOCK
         low = Lowerer(ity, params)
         body = "\n    ".join(low.statements(stmts, init_value))
-        src = f"""extern "C" __global__ void __launch_bounds__({BLOCK}) {KNAME}({_params_decl(params)}{', ' if params.slots else ''}unsigned long long n_) {{
-  const {ity} _global_id = ({ity})blockIdx.x * {BLOCK}u + threadIdx.x;
+        src = f"""extern "C" __global__ void __launch_bounds__({block}) {KNAME}({_params_decl(params)}{', ' if params.slots else ''}unsigned long long n_) {{
+  const {ity} _global_id = ({ity})blockIdx.x * {block}u + threadIdx.x;
   if (_global_id >= ({ity})n_) return;
   {setup}
   {body}
 }}
 """
-        grid = (max(1, ceil(n / BLOCK)), 1, 1)
+        grid = (max(1, ceil(n / block)), 1, 1)
     else:
+        block = BLOCK
         src = _vector_source(stmts, ity, params, setup, index_kind)
         grid = (max(1, ceil(n / (4 * BLOCK))), 1, 1)
-    return KernelPlan(src, grid, (BLOCK, 1, 1), _plan_args(params, (n,)), family="elw", flops=flops)
+    return KernelPlan(src, grid, (block, 1, 1), _plan_args(params, (n,)), family="elw", flops=flops)
 
 
 def _vector_source(stmts, ity, params: Params, setup="", index_kind="global") -> str:
@@ -900,21 +907,29 @@ def dp_config(M, N, K):
     """Block tile and K split of a DotProd: 64-wide tiles on a narrow side,
     128 otherwise (256 x 128 measured slower at 4096^3 and in the C5 step),
     and 64 x 64 for a short K (<= 128), where the epilogue's HBM traffic
-    dominates and more, smaller blocks keep more of it in flight;
+    dominates and more, smaller blocks keep more of it in flight, and for
+    products of at most 512 x 512 outputs (the per-head attention products,
+    launched many at a time: more blocks per compute unit hide latency);
     K is split (up to 16 chunks of at least 256) while the
     tiles alone would not give one block per compute unit, and a long K
     (chunks of at least 1024) is split once more until two blocks share
     each compute unit (one block's barriers then hide behind the other's
     products)."""
-    BM = 64 if M <= 64 or K <= 128 else 128
-    BN = 64 if N <= 64 or K <= 128 else 128
+    small = K <= 128 or M * N <= (1 << 18)
+    BM = 64 if M <= 64 or small else 128
+    BN = 64 if N <= 64 or small else 128
     tiles = ceil(M / BM) * ceil(N / BN)
     split = 1
     while tiles * split < 256 and split < 16 and K // (2 * split) >= 256:
         split *= 2
     while tiles * split < 512 and split < 16 and K // (2 * split) >= 1024:
         split *= 2
-    return BM, BN, split
+    return BM, BN, split, dp_panel(M, N, K, BM, BN, split)
+
+
+def dp_panel(M, N, K, BM, BN, split):
+    """Depth of the K panels staged in LDS."""
+    return 16
 
 
 VEC_HOIST_MAX = 4
@@ -942,7 +957,7 @@ def dotprod_plan(stmts, dp, A=None, B=None, config=None, partial_off=None) -> Ke
     unsplit product whose epilogue runs as a separate pass."""
     M, N = dp.shape
     K = dp.children_shapes[0][1]
-    BM, BN, split = config if config is not None else dp_config(M, N, K)
+    BM, BN, split, BK = config if config is not None else dp_config(M, N, K)
     A = dp.kargs[0] if A is None else A
     B = dp.kargs[1] if B is None else B
     bound = _expr_bound(stmts, M * N, max(M, K), max(N, K))
@@ -993,7 +1008,7 @@ def dotprod_plan(stmts, dp, A=None, B=None, config=None, partial_off=None) -> Ke
     init = _init_list(params)
     src = ((la + lb + epi).replace("@FIELDS@", _fields(params)) +
            f"extern \"C\" __global__ void __launch_bounds__(256) {KNAME}({_params_decl(params)}) {{\n"
-           f"  adhip::dp_mfma<{BM}, {BN}, {split}>(LA{{{init}}}, LB{{{init}}}, EPI{{{init}}}, {M}, {N}, {K});\n}}\n")
+           f"  adhip::dp_mfma<{BM}, {BN}, {split}, {BK}>(LA{{{init}}}, LB{{{init}}}, EPI{{{init}}}, {M}, {N}, {K});\n}}\n")
     grid = (ceil(N / BN), ceil(M / BM) * split, 1)
     return KernelPlan(src, grid, (256, 1, 1), _plan_args(params), family="dotprod",
                       flops=2 * M * N * K)
@@ -1016,18 +1031,32 @@ def tree_inclusion(R):
     return sorted(sets[0])
 
 
+def _cols_vec(red) -> bool:
+    """A column-mode Reduce can load 4 consecutive columns as one float4:
+    the kept axis is contiguous and 4-aligned, and no row is dropped by the
+    reference's tree."""
+    V, R = red.children_shapes[0]
+    karg = red.kargs[0]
+    if not isinstance(karg, KMatrix) or V % 4 != 0 or len(tree_inclusion(R)) < R:
+        return False
+    core, c = split_const(karg.access)
+    vx = vec_class(core, X)
+    return vx.kind == AFF and vx.al and c % 4 == 0
+
+
 def reduce_mode(red):
     """``("rows"|"cols", split)`` for a Reduce: rows when the reduced axis is
-    contiguous, cols when the kept axis is; columns are split over blocks
-    when too few column blocks would fill the device."""
+    contiguous, cols when the kept axis is; rows are split into chunks over
+    blocks until there are 512 blocks (two per compute unit; HBM needs that
+    many loads in flight)."""
     V, R = red.children_shapes[0]
     karg = red.kargs[0]
     if isinstance(karg, KMatrix):
         core, _ = split_const(karg.access)
         if vec_class(core, Y).kind != AFF and vec_class(core, X).kind == AFF:
-            blocks = ceil(V / 64)
+            blocks = ceil(V / (256 if _cols_vec(red) else 64))
             split = 1
-            while blocks * split < 512 and split < 64 and R // (2 * split) >= 64:
+            while blocks * split < 512 and split < 128 and R // (2 * split) >= 64:
                 split *= 2
             return "cols", split
     return "rows", 1
@@ -1075,7 +1104,9 @@ def reduce_plan(stmts, red, partial_off=None) -> KernelPlan:
                   f"return (t[y >> 5] >> (y & 31)) & 1u; }}\n")
     else:
         inc_fn = f"  __device__ bool inc({ity}) const {{ return true; }}\n"
-    ld = (f"struct LD {{ static constexpr bool kVec = {'true' if vec else 'false'}; @FIELDS@\n"
+    vecx = mode == "cols" and _cols_vec(red)
+    ld = (f"struct LD {{ static constexpr bool kVec = {'true' if vec else 'false'}; "
+          f"static constexpr bool kVecX = {'true' if vecx else 'false'}; @FIELDS@\n"
           f"  __device__ float at({ity} _x, {ity} _y) const {{ (void)_x; (void)_y; {at} }}\n"
           f"  __device__ float4 at4({ity} _x, {ity} _y) const {{ (void)_x; (void)_y; {at4} }}\n{inc_fn}}};\n")
     if partial_off is not None:
@@ -1098,7 +1129,7 @@ def reduce_plan(stmts, red, partial_off=None) -> KernelPlan:
            f"  {call}(LD{{{init}}}, EPI{{{init}}}, {V}u, {R}u, {'true' if pad_zero else 'false'});\n}}\n")
     # rows: 4 waves per block, at most 2048 blocks (8 per compute unit); the
     # waves stride over the remaining rows
-    grid = (min(ceil(V / 4), 2048), 1, 1) if mode == "rows" else (ceil(V / 64), split, 1)
+    grid = (min(ceil(V / 4), 2048), 1, 1) if mode == "rows" else (ceil(V / (256 if vecx else 64)), split, 1)
     return KernelPlan(src, grid, (256, 1, 1), _plan_args(params), family="reduce",
                       bytes=4 * V * R + 4 * V)
 
