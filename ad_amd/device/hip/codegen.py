@@ -835,9 +835,11 @@ def _vector_lines(stmts, ity, params: Params, index_kind="global", hoist=None) -
                 for lane in "xyzw":
                     lines.append(f"_value.{lane} = fmaxf(_value.{lane}, 0.0f);")
             continue
-        # operands are loaded before the statement computes (program order)
-        for k in n.kargs:
-            operand(k)
+        # operands are loaded before the statement computes (program order);
+        # an init statement's value is the product or reduction itself
+        if kind != "init":
+            for k in n.kargs:
+                operand(k)
         vals = [rhs(kind, n, i) for i in range(4)]
         if n.kres.is_temp:
             for i in range(4):

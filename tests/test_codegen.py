@@ -288,3 +288,45 @@ def test_combine_passes_follow_a_partial_store():
                 assert any(a in prev.args for a in slot)
     assert combines > 0
     ad.reset()
+
+
+def test_dotprod_epilogues_load_only_epilogue_operands():
+    """The operand registers an in-kernel DotProd epilogue fills before its
+    statements hold only what the epilogue statements read: never the
+    product's own A and B operands (indexed as the output, they would read
+    past those operands)."""
+    import ad_amd as ad
+    from ad_amd import workloads
+    from ad_amd.alloc import AllocEntry
+    from ad_amd.fusion import DPElwFuse
+    from ad_amd.graph import DotProdNode, ForNode, Receiver, Tensor
+    ad.reset()
+    workloads.transformer(layers=1, d_model=64, heads=4, ff=64, seq=8, batch=2, steps=1, receive=False)
+    rng = np.random.default_rng(0)
+    a, b = Tensor(rng.standard_normal((64, 32)).astype(np.float32)), Tensor(rng.standard_normal((32, 64)).astype(np.float32))
+    Receiver(lambda v: None, [a @ b])
+    proc = ad.compile_proc()
+    info = codegen.BufferInfo()
+
+    def note(c, _):
+        if isinstance(c, AllocEntry):
+            info.size[c.id] = c.size
+        return c
+    proc.walk(note, step_fused=False, step_proc=True)
+    cmds = list(proc.procedure)
+    for c in proc.procedure:
+        if isinstance(c, ForNode):
+            cmds.extend(c.get_proc().procedure)
+    checked = 0
+    for cmd in cmds:
+        if not isinstance(cmd, (DPElwFuse, DotProdNode)):
+            continue
+        stmts = codegen.statements(cmd.nodes if isinstance(cmd, DPElwFuse) else [cmd])
+        for p in codegen.command_plans(cmd, info, 0)[0]:
+            if p.family != "dotprod" or "kLoads = " not in p.source:
+                continue
+            n = int(p.source.split("kLoads = ")[1].split(";")[0])
+            assert n <= codegen.epilogue_loads(stmts), p.source
+            checked += 1
+    assert checked > 0
+    ad.reset()
