@@ -9,9 +9,9 @@
 //                    into chunks, epilogue in registers.
 //  * reduce_rows  -- Reduce+Elw, rows contiguous: waves striding over rows,
 //                    float4 or scalar coalesced loads, butterfly over the wave.
-//  * reduce_cols  -- Reduce+Elw, columns contiguous: 64 or 256 (float4)
-//                    columns x 4 row groups per block, coalesced along the
-//                    columns, LDS combine, optional split of the rows.
+//  * reduce_cols  -- Reduce+Elw, columns contiguous: 64 columns x 4 or 16
+//                    (float4 lanes) row groups per block, coalesced along
+//                    the columns, LDS combine, optional split of the rows.
 // Elementwise (ElwFuse) kernels are emitted whole by the generator.
 #pragma clang fp contract(off)
 
@@ -317,20 +317,23 @@ __device__ __forceinline__ void reduce_rows(const LD& ld, const EPI& epi, unsign
   }
 }
 
-// reduce_cols: a block covers 64*W columns (W = 4 consecutive columns per
-// lane loaded as one float4 when LD::kVecX, else 1) and 4 row groups, one
-// per wave (group g takes rows g, g+4, ...); a lane keeps 8 rows' loads in
-// flight; the 4 groups combine through LDS.  SPLIT > 1 splits the rows into
-// SPLIT chunks (blockIdx.y) whose results go to the epilogue with the chunk
-// index and without the zero padding of MAX (applied once the chunks are
-// combined).  Every column sums its rows in order within a group.
+// reduce_cols: a block covers 64 columns and G row groups: with LD::kVecX
+// 16 lanes per group load 4 consecutive columns each as one float4
+// (G = 16), else 64 lanes load one column each (G = 4); group g takes rows
+// g, g+G, ..., a lane keeps 8 rows' loads in flight, and the groups combine
+// through LDS in order.  SPLIT > 1 splits the rows into SPLIT chunks
+// (blockIdx.y) whose results go to the epilogue with the chunk index and
+// without the zero padding of MAX (applied once the chunks are combined).
 template <int OP, int SPLIT, class LD, class EPI>
 __device__ __forceinline__ void reduce_cols(const LD& ld, const EPI& epi, unsigned V, unsigned R,
                                             bool pad_zero) {
-  constexpr int W = LD::kVecX ? 4 : 1;
-  __shared__ float part[4][64 * W];
-  const unsigned lane = threadIdx.x & 63, grp = threadIdx.x >> 6;
-  const unsigned col0 = blockIdx.x * (64 * W) + lane * W;
+  constexpr int W = LD::kVecX ? 4 : 1;         // columns per lane
+  constexpr int L = 64 / W;                    // lanes per row group
+  constexpr int G = 256 / L;                   // row groups per block
+  __shared__ float part[G][64];
+  const unsigned t = threadIdx.x;
+  const unsigned grp = t / L, sub = t % L;
+  const unsigned col0 = blockIdx.x * 64 + sub * W;
   unsigned ybeg = 0, yend = R;
   if constexpr (SPLIT > 1) {
     const unsigned rc = (R + SPLIT - 1) / SPLIT;
@@ -345,10 +348,10 @@ __device__ __forceinline__ void reduce_cols(const LD& ld, const EPI& epi, unsign
     // V % 4 == 0: a lane's 4 columns are all in range or all out
     if (col0 < V) {
       unsigned y = ybeg + grp;
-      for (; y + 28 < yend; y += 32) {
+      for (; y + 7 * G < yend; y += 8 * G) {
         float4 v[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = ld.at4(col0, y + 4 * u);
+        for (int u = 0; u < 8; ++u) v[u] = ld.at4(col0, y + G * u);
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
           acc[0] = rop<OP>(acc[0], v[u].x);
@@ -357,7 +360,7 @@ __device__ __forceinline__ void reduce_cols(const LD& ld, const EPI& epi, unsign
           acc[3] = rop<OP>(acc[3], v[u].w);
         }
       }
-      for (; y < yend; y += 4) {
+      for (; y < yend; y += G) {
         const float4 v = ld.at4(col0, y);
         acc[0] = rop<OP>(acc[0], v.x);
         acc[1] = rop<OP>(acc[1], v.y);
@@ -367,16 +370,18 @@ __device__ __forceinline__ void reduce_cols(const LD& ld, const EPI& epi, unsign
     }
   } else {
     if (col0 < V)
-      for (unsigned y = ybeg + grp; y < yend; y += 4)
+      for (unsigned y = ybeg + grp; y < yend; y += G)
         if (ld.inc(y)) acc[0] = rop<OP>(acc[0], ld.at(col0, y));
   }
 #pragma unroll
-  for (int w = 0; w < W; ++w) part[grp][lane * W + w] = acc[w];
+  for (int w = 0; w < W; ++w) part[grp][sub * W + w] = acc[w];
   __syncthreads();
-  for (unsigned t = threadIdx.x; t < 64u * W; t += blockDim.x) {
-    const unsigned col = blockIdx.x * (64 * W) + t;
+  if (t < 64) {
+    const unsigned col = blockIdx.x * 64 + t;
     if (col < V) {
-      float a = rop<OP>(rop<OP>(rop<OP>(part[0][t], part[1][t]), part[2][t]), part[3][t]);
+      float a = part[0][t];
+#pragma unroll
+      for (int g = 1; g < G; ++g) a = rop<OP>(a, part[g][t]);
       if (SPLIT == 1 && OP == 1 && pad_zero) a = fmaxf(a, 0.f);
       epi(a, col, (int)blockIdx.y);
     }

@@ -667,13 +667,8 @@ def elementwise_plan(stmts, n, index_kind="global", n_cols=1, flops=0, init_valu
     bound = _expr_bound(stmts, max(n - 1, 0), max(n - 1, 0), max(n_cols - 1, 0))
     ity = _ity(bound)
     setup = _index_setup(index_kind, ity, n_cols)
-    # combining many partial results for few elements: one element per
-    # thread in 64-thread blocks spreads the partials' loads over more
-    # compute units than a few 256-thread blocks of float4 lanes would
-    many_partials = any(k == "sum" and node[1] >= 16 for k, node in stmts)
-    narrow = many_partials and ceil(n / (4 * BLOCK)) < 64
-    if narrow or not _vector_plan(stmts, n, index_kind, n_cols):
-        block = 64 if narrow else BLOCK
+    if not _vector_plan(stmts, n, index_kind, n_cols):
+        block = BLOCK
         low = Lowerer(ity, params)
         body = "\n    ".join(low.statements(stmts, init_value))
         src = f"""extern "C" __global__ void __launch_bounds__({block}) {KNAME}({_params_decl(params)}{', ' if params.slots else ''}unsigned long long n_) {{
@@ -1056,7 +1051,7 @@ def reduce_mode(red):
     if isinstance(karg, KMatrix):
         core, _ = split_const(karg.access)
         if vec_class(core, Y).kind != AFF and vec_class(core, X).kind == AFF:
-            blocks = ceil(V / (256 if _cols_vec(red) else 64))
+            blocks = ceil(V / 64)
             split = 1
             while blocks * split < 512 and split < 128 and R // (2 * split) >= 64:
                 split *= 2
@@ -1131,7 +1126,7 @@ def reduce_plan(stmts, red, partial_off=None) -> KernelPlan:
            f"  {call}(LD{{{init}}}, EPI{{{init}}}, {V}u, {R}u, {'true' if pad_zero else 'false'});\n}}\n")
     # rows: 4 waves per block, at most 2048 blocks (8 per compute unit); the
     # waves stride over the remaining rows
-    grid = (min(ceil(V / 4), 2048), 1, 1) if mode == "rows" else (ceil(V / (256 if vecx else 64)), split, 1)
+    grid = (min(ceil(V / 4), 2048), 1, 1) if mode == "rows" else (ceil(V / 64), split, 1)
     return KernelPlan(src, grid, (256, 1, 1), _plan_args(params), family="reduce",
                       bytes=4 * V * R + 4 * V)
 

@@ -16,8 +16,9 @@
   [8192,4096]) and ElwFuse (6 ops over 64M floats) commands, HBM-bound, with
   inputs rotated across copies larger than the 256 MB last-level cache.
 * ``other_configs``: C1 (the MLP of examples/linear.py, a Feeder upload per
-  step), C3 (LayerNorm fwd+bwd at [16384,1024], GB/s over its 5-pass HBM
-  floor) and C4 (1-layer transformer) at full size, graph-replayed.
+  step), C3 (LayerNorm fwd+bwd at [16384,1024], GB/s over the Proc's
+  per-command bytes and over the 5-pass HBM floor) and C4 (1-layer
+  transformer) at full size, graph-replayed.
 * ``cpu_baseline``: the CPU restatement of the reference OpenCL backend
   (``oracle``, one OpenMP iteration per work-item, sequential k-loops) timed
   on this host on a bounded sample of the same workload (the step's FFN
@@ -214,6 +215,13 @@ def loop_rate(build, steps, warmup):
 # bytes of the 5-pass floor of one LayerNorm fwd+bwd iteration at [16384, 1024]:
 # five passes over a 64 MiB matrix
 C3_FLOOR_BYTES = 5 * 4 * 16384 * 1024
+# algorithmic bytes of the iteration's Proc, per command (each distinct operand
+# at its true size): row mean (x in, mean out); beta grad (dy in, beta in+out);
+# x - mean and its square (x, mean in; two matrices out); 1/sqrt(var + eps)
+# (squares in, rstd out); dy * xhat (xc, rstd, dy in; one matrix out); gamma
+# grad (that matrix in, gamma in+out): ten 64 MiB matrix passes, four 64 KiB
+# row vectors, four 4 KiB parameter vectors
+C3_PROC_BYTES = 10 * 4 * 16384 * 1024 + 4 * 4 * 16384 + 4 * 4 * 1024
 
 
 def other_configs():
@@ -228,11 +236,15 @@ def other_configs():
     log(f"c1: {c1['ms'] * 1e3:.1f} us/step, {c1['launches']} launches/step")
     c3 = loop_rate(lambda: workloads.layernorm_train(rows=16384, cols=1024, steps=1, receive=False), 50, 3)
     gbs = C3_FLOOR_BYTES / c3["ms"] / 1e6
+    pgbs = C3_PROC_BYTES / c3["ms"] / 1e6
     out["c3_layernorm"] = {"workload": "LayerNorm fwd+bwd [16384,1024] + SGD on gamma/beta",
-                           "ms_per_iter": round(c3["ms"], 4), "floor_bytes": C3_FLOOR_BYTES,
-                           "floor_gbs": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4),
+                           "ms_per_iter": round(c3["ms"], 4),
+                           "proc_bytes": C3_PROC_BYTES, "proc_gbs": round(pgbs, 1),
+                           "frac": round(pgbs / PEAK_HBM_GBS, 4),
+                           "floor_bytes": C3_FLOOR_BYTES, "floor_gbs": round(gbs, 1),
                            "launches_per_iter": c3["launches"]}
-    log(f"c3: {c3['ms'] * 1e3:.1f} us/iter, {gbs:.0f} GB/s over the 5-pass floor")
+    log(f"c3: {c3['ms'] * 1e3:.1f} us/iter, {pgbs:.0f} GB/s over the Proc's bytes, "
+        f"{gbs:.0f} GB/s over the 5-pass floor")
     c4 = transformer_steps("c4", 20, 3)
     ms = c4["event_ms"] / 20
     out["c4_transformer"] = {"workload": "1-layer encoder d_model 512, 8 heads, FFN 2048, seq 256, batch 16",
