@@ -34,7 +34,9 @@ __device__ __forceinline__ float rop(float a, float b) {
 // Block tile BM x BN, K panels of BK staged in two LDS buffers, 4 waves as
 // 2 x 2, each wave (BM/2) x (BN/2) made of 32x32 v_mfma_f32_32x32x2f32 tiles;
 // the next panel is prefetched into registers while the current one is
-// consumed, then stored into the other buffer.
+// consumed, then stored into the other buffer.  A lane reads its operand
+// fragments for 4 MFMA steps at a time (one float4 per 32-row tile for an
+// operand kept k-contiguous in LDS).
 // SPLIT > 1 splits K into SPLIT chunks: blockIdx.y = tile row + tiles_m *
 // chunk, and the epilogue receives the chunk index (partial results).
 // Epilogue, EPI::kVec4 false: per 32x32 tile, epi.load(row, col, l) fills
@@ -45,7 +47,7 @@ __device__ __forceinline__ float rop(float a, float b) {
 // epi.load4(row, col, l) fills float4 operand registers for the lane's 4
 // groups, then epi.vec(value4, row, col, chunk, l) runs the statements on 4
 // elements with float4 loads and stores.
-constexpr int DP_PAD = 4, DP_GROUP = 8, DP_CPITCH = 40;
+constexpr int DP_GROUP = 8, DP_CPITCH = 40;
 
 template <int BM, int BN, int SPLIT, int BK, class LA, class LB, class EPI>
 __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& epi, int M, int N, int K) {
@@ -55,14 +57,27 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
   constexpr int VA = BM * BK / 4 / 256;               // float4 loads per thread
   constexpr int VB = BN * BK / 4 / 256;
   static_assert(VA >= 1 && VB >= 1, "tile too small for 256 threads");
+  // LDS layout of a K panel: an operand contiguous along k in memory (A
+  // kMode 0, B kMode 1) is kept as [row][k] (pitch KP = BK + 4 floats), so a
+  // lane reads the 4 consecutive k of 4 MFMA steps as one float4; the other
+  // as [k][row] (pitch rows + 4), read as scalars.  Panel loads and stores
+  // are float4s along the contiguous axis.  (Transposing the second operand
+  // into [row][k] too needs k-fastest lanes for conflict-free stores, which
+  // breaks the coalescing of its loads: measured slower.)
   // K panels (two buffers of A and of B) and, after the products, the
-  // per-wave 32x32 staging of the vectorised epilogue share one LDS block
-  constexpr int A_FLOATS = 2 * BK * (BM + DP_PAD), B_FLOATS = 2 * BK * (BN + DP_PAD);
+  // per-wave 32x32 staging of the vectorised epilogue share one LDS block.
+  constexpr bool AR = LA::kMode == 0, BR = LB::kMode == 1;
+  constexpr int KP = BK + 4, H = BK / 2;
+  constexpr int APITCH = AR ? KP : BM + 4, BPITCH = BR ? KP : BN + 4;
+  constexpr int A_FLOATS = 2 * (AR ? BM : BK) * APITCH, B_FLOATS = 2 * (BR ? BN : BK) * BPITCH;
   constexpr int C_FLOATS = EPI::kVec4 ? 4 * 32 * DP_CPITCH : 0;
   constexpr int S_FLOATS = A_FLOATS + B_FLOATS > C_FLOATS ? A_FLOATS + B_FLOATS : C_FLOATS;
   __shared__ __attribute__((aligned(16))) float smem[S_FLOATS];
-  float (*As)[BK][BM + DP_PAD] = reinterpret_cast<float (*)[BK][BM + DP_PAD]>(smem);
-  float (*Bs)[BK][BN + DP_PAD] = reinterpret_cast<float (*)[BK][BN + DP_PAD]>(smem + A_FLOATS);
+  float* const As = smem;
+  float* const Bs = smem + A_FLOATS;
+  // float offset of element (row, k) of panel buffer `buf`
+  auto a_off = [](int buf, int m, int k) { return AR ? (buf * BM + m) * APITCH + k : (buf * BK + k) * APITCH + m; };
+  auto b_off = [](int buf, int n, int k) { return BR ? (buf * BN + n) * BPITCH + k : (buf * BK + k) * BPITCH + n; };
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -93,12 +108,23 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
 
   float ra[VA][4], rb[VB][4];
 
+  // float4 v of a panel (v < rows * BK / 4): (row, k) of its first float
+  auto a_pos = [](int v, int& m, int& k) {
+    if constexpr (AR) { m = v / (BK / 4); k = 4 * (v % (BK / 4)); }
+    else { k = v / (BM / 4); m = 4 * (v % (BM / 4)); }
+  };
+  auto b_pos = [](int v, int& n, int& k) {
+    if constexpr (BR) { n = v / (BK / 4); k = 4 * (v % (BK / 4)); }
+    else { k = v / (BN / 4); n = 4 * (v % (BN / 4)); }
+  };
   auto load_a = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < VA; ++i) {
-      const int v = tid + 256 * i;
-      if constexpr (LA::kMode == 0) {          // row of 4 consecutive k
-        const int m = m0 + v / (BK / 4), k = k0 + 4 * (v % (BK / 4));
+      int m, k;
+      a_pos(tid + 256 * i, m, k);
+      m += m0;
+      k += k0;
+      if constexpr (LA::kMode == 0) {          // 4 consecutive k of row m
         if constexpr (LA::kVec) {
           const float4 x = (m < M && k < kend) ? la.at4(m, k) : make_float4(0.f, 0.f, 0.f, 0.f);
           ra[i][0] = x.x; ra[i][1] = x.y; ra[i][2] = x.z; ra[i][3] = x.w;
@@ -106,8 +132,7 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
 #pragma unroll
           for (int j = 0; j < 4; ++j) ra[i][j] = (m < M && k + j < kend) ? la.at(m, k + j) : 0.f;
         }
-      } else {                                  // k row of 4 consecutive m
-        const int k = k0 + v / (BM / 4), m = m0 + 4 * (v % (BM / 4));
+      } else {                                  // 4 consecutive m of k row
         if constexpr (LA::kVec) {
           const float4 x = (k < kend && m < M) ? la.at4(m, k) : make_float4(0.f, 0.f, 0.f, 0.f);
           ra[i][0] = x.x; ra[i][1] = x.y; ra[i][2] = x.z; ra[i][3] = x.w;
@@ -121,23 +146,19 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
   auto store_a = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < VA; ++i) {
-      const int v = tid + 256 * i;
-      if constexpr (LA::kMode == 0) {
-        const int m = v / (BK / 4), k = 4 * (v % (BK / 4));
-#pragma unroll
-        for (int j = 0; j < 4; ++j) As[buf][k + j][m] = ra[i][j];
-      } else {
-        const int k = v / (BM / 4), m = 4 * (v % (BM / 4));
-        *reinterpret_cast<float4*>(&As[buf][k][m]) = make_float4(ra[i][0], ra[i][1], ra[i][2], ra[i][3]);
-      }
+      int m, k;
+      a_pos(tid + 256 * i, m, k);
+      *reinterpret_cast<float4*>(As + a_off(buf, m, k)) = make_float4(ra[i][0], ra[i][1], ra[i][2], ra[i][3]);
     }
   };
   auto load_b = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < VB; ++i) {
-      const int v = tid + 256 * i;
-      if constexpr (LB::kMode == 0) {          // k row of 4 consecutive n
-        const int k = k0 + v / (BN / 4), n = n0 + 4 * (v % (BN / 4));
+      int n, k;
+      b_pos(tid + 256 * i, n, k);
+      n += n0;
+      k += k0;
+      if constexpr (LB::kMode == 0) {          // 4 consecutive n of k row
         if constexpr (LB::kVec) {
           const float4 x = (k < kend && n < N) ? lb.at4(k, n) : make_float4(0.f, 0.f, 0.f, 0.f);
           rb[i][0] = x.x; rb[i][1] = x.y; rb[i][2] = x.z; rb[i][3] = x.w;
@@ -145,8 +166,7 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
 #pragma unroll
           for (int j = 0; j < 4; ++j) rb[i][j] = (k < kend && n + j < N) ? lb.at(k, n + j) : 0.f;
         }
-      } else {                                  // column of 4 consecutive k
-        const int n = n0 + v / (BK / 4), k = k0 + 4 * (v % (BK / 4));
+      } else {                                  // 4 consecutive k of column n
         if constexpr (LB::kVec) {
           const float4 x = (n < N && k < kend) ? lb.at4(k, n) : make_float4(0.f, 0.f, 0.f, 0.f);
           rb[i][0] = x.x; rb[i][1] = x.y; rb[i][2] = x.z; rb[i][3] = x.w;
@@ -160,15 +180,9 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
   auto store_b = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < VB; ++i) {
-      const int v = tid + 256 * i;
-      if constexpr (LB::kMode == 0) {
-        const int k = v / (BN / 4), n = 4 * (v % (BN / 4));
-        *reinterpret_cast<float4*>(&Bs[buf][k][n]) = make_float4(rb[i][0], rb[i][1], rb[i][2], rb[i][3]);
-      } else {
-        const int n = v / (BK / 4), k = 4 * (v % (BK / 4));
-#pragma unroll
-        for (int j = 0; j < 4; ++j) Bs[buf][k + j][n] = rb[i][j];
-      }
+      int n, k;
+      b_pos(tid + 256 * i, n, k);
+      *reinterpret_cast<float4*>(Bs + b_off(buf, n, k)) = make_float4(rb[i][0], rb[i][1], rb[i][2], rb[i][3]);
     }
   };
 
@@ -197,18 +211,42 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
         load_a(k0 + BK);
         load_b(k0 + BK);
       }
+      // MFMA step s of the panel multiplies k = H * (lane / 32) + s: a lane
+      // takes H consecutive k (any assignment of the panel's k to steps and
+      // lane halves is a valid order of the sum, the same for A and B);
+      // fragments are read 4 steps at a time
 #pragma unroll
-      for (int kk = 0; kk < BK; kk += 2) {
-        float a[TM], b[TN];
+      for (int q = 0; q < H / 4; ++q) {
+        float af[TM][4], bf[TN][4];
 #pragma unroll
-        for (int i = 0; i < TM; ++i) a[i] = As[cur][kk + lk][wm * (BM / 2) + i * 32 + lr];
+        for (int i = 0; i < TM; ++i) {
+          const int m = wm * (BM / 2) + i * 32 + lr;
+          if constexpr (AR) {
+            const float4 x = *reinterpret_cast<const float4*>(As + a_off(cur, m, H * lk + 4 * q));
+            af[i][0] = x.x; af[i][1] = x.y; af[i][2] = x.z; af[i][3] = x.w;
+          } else {
 #pragma unroll
-        for (int j = 0; j < TN; ++j) b[j] = Bs[cur][kk + lk][wn * (BN / 2) + j * 32 + lr];
+            for (int st = 0; st < 4; ++st) af[i][st] = As[a_off(cur, m, H * lk + 4 * q + st)];
+          }
+        }
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+        for (int j = 0; j < TN; ++j) {
+          const int n = wn * (BN / 2) + j * 32 + lr;
+          if constexpr (BR) {
+            const float4 x = *reinterpret_cast<const float4*>(Bs + b_off(cur, n, H * lk + 4 * q));
+            bf[j][0] = x.x; bf[j][1] = x.y; bf[j][2] = x.z; bf[j][3] = x.w;
+          } else {
 #pragma unroll
-          for (int j = 0; j < TN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+            for (int st = 0; st < 4; ++st) bf[j][st] = Bs[b_off(cur, n, H * lk + 4 * q + st)];
+          }
+        }
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][st], bf[j][st], acc[i][j], 0, 0, 0);
       }
       if (more) {
         store_a(cur ^ 1);
