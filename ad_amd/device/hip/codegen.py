@@ -189,6 +189,23 @@ def _loc_sig(km: KMatrix, index_kind: str, n_cols: int):
     return ("e", repr(core), c)
 
 
+def temp_access_violations(stmts, index_kind: str, n_cols: int = 1):
+    """Temps read through an access that is not the element's own location,
+    as ``(statement index, temp id, access text)``.  The reference lowers a
+    temp operand to its register whatever the access (karg.py:47-48), so a
+    fused node reading an in-group temp through, e.g., a permute silently
+    reads its own element's value instead."""
+    out = []
+    for si, (kind, n) in enumerate(stmts):
+        if kind in ("tmp", "load", "store", "sum", "init"):
+            continue
+        for k in n.kargs:
+            for km in _iter_kmatrix(k):
+                if km.is_temp and _loc_sig(km, index_kind, n_cols) != ("g", 0):
+                    out.append((si, km.id, repr(km.access)))
+    return out
+
+
 def conflict_pairs(stmts, buffers: BufferInfo, index_kind: str, n_cols: int = 1):
     """Pairs ``(i, j)``, ``i <= j``, of statement indices that must not run
     in the same pass over the elements: some element's access in one may
@@ -1028,13 +1045,21 @@ def tree_inclusion(R):
     return sorted(sets[0])
 
 
-def _cols_vec(red) -> bool:
+def kept_elements(R, exact=False):
+    """Indices of a row that a reduction combines: those reaching the
+    reference's tree (``tree_inclusion``; indices >= R are zero padding), or
+    with ``exact`` every one of the R elements and no padding (the fix of the
+    tree for non-power-of-two lengths and of MAX's zero padding)."""
+    return list(range(R)) if exact else tree_inclusion(R)
+
+
+def _cols_vec(red, exact=False) -> bool:
     """A column-mode Reduce can load 4 consecutive columns as one float4:
     the kept axis is contiguous and 4-aligned, and no row is dropped by the
     reference's tree."""
     V, R = red.children_shapes[0]
     karg = red.kargs[0]
-    if not isinstance(karg, KMatrix) or V % 4 != 0 or len(tree_inclusion(R)) < R:
+    if not isinstance(karg, KMatrix) or V % 4 != 0 or len(kept_elements(R, exact)) < R:
         return False
     core, c = split_const(karg.access)
     vx = vec_class(core, X)
@@ -1059,13 +1084,13 @@ def reduce_mode(red):
     return "rows", 1
 
 
-def reduce_plan(stmts, red, partial_off=None) -> KernelPlan:
+def reduce_plan(stmts, red, partial_off=None, exact=False) -> KernelPlan:
     """Row reduction (+ epilogue on the reduced value)
     (kernels/reduce.py:8-66, reduce_elw_fuse.py:12-80 semantics).  When the
     columns are split, the blocks store partial results to scratch at
     ``partial_off`` ([chunk][V]) and ``stmts`` must be empty."""
     V, R = red.children_shapes[0]
-    inc = tree_inclusion(R)
+    inc = kept_elements(R, exact)
     dropped = [y for y in range(R) if y not in set(inc)] if len(inc) < R else []
     pad_zero = any(y >= R for y in inc)
     bound = _expr_bound(stmts, V, V, R)
@@ -1101,7 +1126,7 @@ def reduce_plan(stmts, red, partial_off=None) -> KernelPlan:
                   f"return (t[y >> 5] >> (y & 31)) & 1u; }}\n")
     else:
         inc_fn = f"  __device__ bool inc({ity}) const {{ return true; }}\n"
-    vecx = mode == "cols" and _cols_vec(red)
+    vecx = mode == "cols" and _cols_vec(red, exact)
     ld = (f"struct LD {{ static constexpr bool kVec = {'true' if vec else 'false'}; "
           f"static constexpr bool kVecX = {'true' if vecx else 'false'}; @FIELDS@\n"
           f"  __device__ float at({ity} _x, {ity} _y) const {{ (void)_x; (void)_y; {at} }}\n"
@@ -1132,7 +1157,7 @@ def reduce_plan(stmts, red, partial_off=None) -> KernelPlan:
 
 
 # ------------------------------------------------------------------ lockstep fallback
-def lockstep_plans(stmts, n, index_kind, n_cols, init_node, scratch_base):
+def lockstep_plans(stmts, n, index_kind, n_cols, init_node, scratch_base, exact=False):
     """Exact lockstep semantics for a command with cross-element memory
     dependences: one kernel per statement, each computing its value for every
     element into a staging array before a second kernel stores it.  Temps and
@@ -1146,7 +1171,7 @@ def lockstep_plans(stmts, n, index_kind, n_cols, init_node, scratch_base):
     plans = []
     if init_node is not None:
         sink = _scratch_km(init_off, _identity_access(index_kind, n_cols))
-        plans.extend(first_pass_plans([("init", _ValueSink(sink))], n, init_node, alloc))
+        plans.extend(first_pass_plans([("init", _ValueSink(sink))], n, init_node, alloc, exact))
     for kind, node in stmts:
         if kind == "tmp":
             continue
@@ -1219,8 +1244,10 @@ def _stmt_plan(kind, node, n, index_kind, n_cols, temp_off, stage_off, init_off,
 
 
 # ------------------------------------------------------------------ per-command entry
-def command_plans(cmd, buffers: BufferInfo, scratch_base: int):
-    """Plans for one Proc command and the scratch floats they need."""
+def command_plans(cmd, buffers: BufferInfo, scratch_base: int, exact_reduce: bool = False):
+    """Plans for one Proc command and the scratch floats they need.  With
+    ``exact_reduce`` every reduction combines all of its elements (see
+    ``kept_elements``)."""
     if isinstance(cmd, (BinaryNode, UnaryNode, ContigiousNode)):
         stmts, n, kind, cols, init = statements([cmd]), prod(cmd.shape), "global", 1, None
     elif isinstance(cmd, ElwFuse):
@@ -1245,9 +1272,9 @@ def command_plans(cmd, buffers: BufferInfo, scratch_base: int):
     for group in groups:
         pairs = conflict_pairs(group, buffers, kind, cols)
         if any(i == j for i, j in pairs):
-            ps, need = lockstep_plans(group, n, kind, cols, init, end)
+            ps, need = lockstep_plans(group, n, kind, cols, init, end, exact_reduce)
         else:
-            ps, need = phased_plans(group, pairs, n, kind, cols, init, end)
+            ps, need = phased_plans(group, pairs, n, kind, cols, init, end, exact_reduce)
         reads, writes = stmt_regions(group, buffers) if len(groups) > 1 else (None, None)
         for p in ps:
             p.reads, p.writes = reads, writes
@@ -1319,7 +1346,7 @@ def epilogue_loads(part):
     return len(seen)
 
 
-def first_pass_plans(part, n, init_node, alloc: ScratchAlloc):
+def first_pass_plans(part, n, init_node, alloc: ScratchAlloc, exact=False):
     """Plans of the pass that runs the DotProd or Reduce of a command with
     ``part`` as its epilogue: operand gathers, then the product (or the
     reduction) with the epilogue in registers, or -- split over K / rows --
@@ -1348,11 +1375,11 @@ def first_pass_plans(part, n, init_node, alloc: ScratchAlloc):
         return pre + [main, comb]
     mode, split = reduce_mode(init_node)
     if split == 1:
-        return [reduce_plan(part, init_node)]
+        return [reduce_plan(part, init_node, exact=exact)]
     V, R = init_node.children_shapes[0]
-    pad_zero = any(y >= R for y in tree_inclusion(R))
+    pad_zero = any(y >= R for y in kept_elements(R, exact))
     poff = alloc.take(split * V)
-    main = reduce_plan([], init_node, partial_off=poff)
+    main = reduce_plan([], init_node, partial_off=poff, exact=exact)
     op = 0 if init_node.op == ReduceOp.SUM else 1
     comb = elementwise_plan([("sum", (poff, split, V, op, pad_zero))] + part, V,
                             index_kind="red", init_value="_value")
@@ -1394,7 +1421,7 @@ def _temp_uses(stmts):
     return reads, assigns
 
 
-def phased_plans(stmts, pairs, n, index_kind, n_cols, init_node, scratch_base=0):
+def phased_plans(stmts, pairs, n, index_kind, n_cols, init_node, scratch_base=0, exact=False):
     """A command whose statements conflict across elements, run as several
     passes over the elements (one kernel each): the first pass is the
     DotProd/Reduce (if any) with the statements up to the first conflict in
@@ -1437,7 +1464,7 @@ def phased_plans(stmts, pairs, n, index_kind, n_cols, init_node, scratch_base=0)
         tail = [("store", (tid, slot[tid])) for tid in sorted(slot) if assigned_in[tid] == pi]
         part = head + body + tail
         if pi == 0 and init_node is not None:
-            plans.extend(first_pass_plans(part, n, init_node, alloc))
+            plans.extend(first_pass_plans(part, n, init_node, alloc, exact))
         else:
             kind = "global" if init_node is None else ("dp" if isinstance(init_node, DotProdNode) else "red")
             plans.append(elementwise_plan(part, n, index_kind=kind, n_cols=n_cols))

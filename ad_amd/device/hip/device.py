@@ -37,7 +37,7 @@ from math import prod
 import numpy as np
 
 from ...alloc import AllocEntry, DeallocEntry
-from ...fusion import FuseBase
+from ...fusion import DPElwFuse, FuseBase, ReduceElwFuse
 from ...graph import Feeder, ForNode, Receiver
 from ...node import Node
 from .. import Device
@@ -71,8 +71,23 @@ class _Launch:
 
 class HIPDevice(Device):
     def __init__(self, device_index: int = 0, use_graphs: bool = True, jit_threads: int = None,
-                 group_launches: bool = True, lanes: int = 1, receiver_lag: int = 0):
+                 group_launches: bool = True, lanes: int = 1, receiver_lag: int = 0,
+                 exact_reduce: bool = False, feeder_offset_zero: bool = False,
+                 strict_temps: bool = False):
         super().__init__()
+        # fixes of reference behaviours, off by default (the reference's results):
+        # exact_reduce: reductions combine all R elements (the reference's
+        #   work-group tree drops elements for non-power-of-two lengths and
+        #   pads MAX with 0, reduce.py:33-43);
+        # feeder_offset_zero: a Feeder writes at offset 0 of its buffer, as the
+        #   OpenCL backend does (cl_helper.py:316,326) -- the default honours
+        #   the arena offset, as the CUDA backend does (cuda_helper.py:117-119);
+        # strict_temps: raise on a fused temp read through a non-identity
+        #   access, which the reference silently reads as the element's own
+        #   value (karg.py:47-48).
+        self.exact_reduce = exact_reduce
+        self.feeder_offset_zero = feeder_offset_zero
+        self.strict_temps = strict_temps
         # Receivers inside a replayed loop: their callbacks run this many
         # iterations after the iteration that produced the data (0: before
         # the next iteration starts, the reference's order; 1: the next
@@ -173,7 +188,9 @@ class HIPDevice(Device):
         # not share scratch and can run in one launch
         plans, regions, needs = {}, {}, {}
         for cmd in self._pending:
-            ps, need, multipass = codegen.command_plans(cmd, info, 0)
+            if self.strict_temps:
+                self._check_temps(cmd)
+            ps, need, multipass = codegen.command_plans(cmd, info, 0, self.exact_reduce)
             plans[cmd.program_id] = ps
             needs[cmd.program_id] = (need + 63) // 64 * 64
             regions[cmd.program_id] = codegen.command_regions(cmd, info)
@@ -252,6 +269,26 @@ class HIPDevice(Device):
             self._schedules[pid_proc] = bind(items)
             self._lane_schedules[pid_proc] = bind(lane_items)
         self._pending = []
+
+    @staticmethod
+    def _check_temps(cmd):
+        if not hasattr(cmd, "nodes"):
+            return
+        init = getattr(cmd, "init_node", None)
+        if isinstance(cmd, DPElwFuse):
+            kind, cols = "dp", init.shape[1]
+        elif isinstance(cmd, ReduceElwFuse):
+            kind, cols = "red", 1
+        else:
+            kind, cols = "global", 1
+        bad = codegen.temp_access_violations(codegen.statements(cmd.nodes), kind, cols)
+        if bad:
+            si, tid, acc = bad[0]
+            raise ValueError(f"fused command {type(cmd).__name__} (program {cmd.program_id}) reads temp "
+                             f"{tid} through the access {acc}; the reference reads that element's own value")
+
+    def _feeder_dst(self, cmd):
+        return self.buffers[cmd.kres.id] + (0 if self.feeder_offset_zero else 4 * cmd.kres.offset)
 
     def _arg_values(self, plan, pid):
         """Argument row of a plan of command ``pid``: ``(True, arena byte
@@ -380,12 +417,11 @@ class HIPDevice(Device):
         if isinstance(cmd, Feeder):
             if self._capturing:
                 # inside a graph: copy this iteration's data from the staging slot
-                dst = self.buffers[cmd.kres.id] + 4 * cmd.kres.offset
-                self.ctx.copy(dst, self._feeder_slots[cmd.id][self._parity], 4 * prod(cmd.shape))
+                self.ctx.copy(self._feeder_dst(cmd), self._feeder_slots[cmd.id][self._parity], 4 * prod(cmd.shape))
                 self._graph_feeders.append(cmd)
                 return
             arr = self._feeder_value(cmd)
-            self.ctx.write(self.buffers[cmd.kres.id] + 4 * cmd.kres.offset, arr)
+            self.ctx.write(self._feeder_dst(cmd), arr)
             return
         if isinstance(cmd, Receiver):
             if self._capturing:

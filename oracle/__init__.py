@@ -32,6 +32,10 @@ pins each part of this restatement (tests/test_oracle.py, test_frontend.py):
   tests/concat_test.py:28-34, powtwo_test.py:18-27, variance_test.py:19-28.
 * config-1 MLP training and softmax attention: float64 closed forms.
 
+* ``exact_reduce=True`` (not the reference; the fix of its tree for
+  non-power-of-two lengths and of MAX's zero padding): float64 sums and
+  exact maxima (test_oracle.py::test_exact_reduce_mode_sums_every_element).
+
 Parity unpinned: ulp-level agreement of ``exp2``/``log2``/``sin`` with the
 reference device's libm (its tests round to 4-5 decimals), and the Feeder
 offset -- the OpenCL backend writes a Feeder at offset 0

@@ -233,10 +233,12 @@ extern "C" void {name}_wi(float** B) {{
 """
 
 
-def _reduce_kernel(name, args, red, stmts, fused) -> str:
+def _reduce_kernel(name, args, red, stmts, fused, exact=False) -> str:
     """kernels/reduce.py:8-66 and reduce_elw_fuse.py:12-80: one work-group of
     ``L = ceil(R/2)*2`` items per row; ``scratch[y] = y < R ? A(x,y) : 0``;
-    tree ``off = L/2, L/4, ... > 0``; item 0 writes and runs the epilogue."""
+    tree ``off = L/2, L/4, ... > 0``; item 0 writes and runs the epilogue.
+    ``exact`` (not the reference: the fix of its tree) combines all R
+    elements in order, SUM from 0 and MAX from -inf."""
     V, R = red.children_shapes[0]
     L = ceil(R / 2) * 2
     a_expr = lower_karg(red.kargs[0])
@@ -244,7 +246,17 @@ def _reduce_kernel(name, args, red, stmts, fused) -> str:
         step = "scratch[_y] += scratch[_y + _offset];"
     else:
         step = "scratch[_y] = std::fmax(scratch[_y], scratch[_y + _offset]);"
-    compute = f"""    #pragma omp parallel
+    if exact:
+        ident, comb = ("0.0f", "_a += v;") if red.op == ReduceOp.SUM else ("-INFINITY", "_a = std::fmax(_a, v);")
+        compute = f"""    #pragma omp parallel for schedule(static)
+    for (int _x = 0; _x < {V}; ++_x) {{
+        float _a = {ident};
+        for (int _y = 0; _y < {R}; ++_y) {{ const float v = {a_expr}; {comb} }}
+        _init[_x] = _a;
+    }}"""
+    else:
+        compute = None
+    compute = compute or f"""    #pragma omp parallel
     {{
     std::vector<float> scratch_v({L});
     float* scratch = scratch_v.data();
@@ -285,7 +297,7 @@ using std::exp2; using std::log2; using std::sin; using std::sqrt; using std::fa
 """
 
 
-def kernel_source(cmd, name):
+def kernel_source(cmd, name, exact_reduce=False):
     """C++ text for one command (the restated ``init_<kind>``)."""
     args = lower_args(cmd)
     if isinstance(cmd, (BinaryNode, UnaryNode, ContigiousNode)):
@@ -298,9 +310,10 @@ def kernel_source(cmd, name):
     if isinstance(cmd, DPElwFuse):
         return args, _dotprod_kernel(name, args, cmd.init_node, _statements(cmd.nodes, None), fused=True)
     if isinstance(cmd, ReduceNode):
-        return args, _reduce_kernel(name, args, cmd, _statements([cmd], None), fused=False)
+        return args, _reduce_kernel(name, args, cmd, _statements([cmd], None), fused=False, exact=exact_reduce)
     if isinstance(cmd, ReduceElwFuse):
-        return args, _reduce_kernel(name, args, cmd.init_node, _statements(cmd.nodes, None), fused=True)
+        return args, _reduce_kernel(name, args, cmd.init_node, _statements(cmd.nodes, None), fused=True,
+                                    exact=exact_reduce)
     raise TypeError(f"Encountered unexpected cmd: {cmd}")
 
 
@@ -327,8 +340,9 @@ class OracleDevice:
     the CPU.  Buffers are numpy float32 arrays; a Tensor's buffer IS its
     ``arr`` (the reference uses CL_MEM_USE_HOST_PTR on a CPU device)."""
 
-    def __init__(self, feeder_offset_zero=False, threads=None, lockstep=True):
+    def __init__(self, feeder_offset_zero=False, threads=None, lockstep=True, exact_reduce=False):
         self.kernels = {}
+        self.exact_reduce = exact_reduce
         self.funcs = {}
         self.buffers = {}
         self.buffers_size = {}
@@ -365,7 +379,7 @@ class OracleDevice:
             return
         if isinstance(cmd, (Node, FuseBase)):
             name = f"k_{cmd.program_id}"
-            args, src = kernel_source(cmd, name)
+            args, src = kernel_source(cmd, name, self.exact_reduce)
             self._pending.append((cmd.program_id, name, args, src))
             return
         raise AssertionError(f"Encountered unexpected cmd: {cmd}")

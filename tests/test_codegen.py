@@ -330,3 +330,28 @@ def test_dotprod_epilogues_load_only_epilogue_operands():
             checked += 1
     assert checked > 0
     ad.reset()
+
+
+def test_temp_read_through_a_permute_is_reported():
+    """The reference reads a fused temp through any access as its own
+    element (karg.py:47-48): x*2 read transposed inside one ElwFuse.  The
+    check names it; identity reads are not reported."""
+    import ad_amd as ad
+    from ad_amd.device.hip.device import HIPDevice
+    from ad_amd.graph import Receiver, Tensor
+    ad.reset()
+    x = Tensor(np.arange(16, dtype=np.float32).reshape(4, 4))
+    y = Tensor(np.ones((4, 4), dtype=np.float32))
+    Receiver(lambda v: None, [((x * 2.0).T() * y).contigious()])
+    Receiver(lambda v: None, [(x * 3.0) * y])
+    proc = ad.compile_proc()
+    fused = [c for c in proc.procedure if hasattr(c, "nodes")]
+    found = [codegen.temp_access_violations(codegen.statements(c.nodes), "global") for c in fused]
+    assert sum(1 for f in found if f) == 1
+    bad = [c for c, f in zip(fused, found) if f][0]
+    with pytest.raises(ValueError, match="through the access"):
+        HIPDevice._check_temps(bad)
+    for c, f in zip(fused, found):
+        if not f:
+            HIPDevice._check_temps(c)
+    ad.reset()

@@ -316,3 +316,49 @@ def test_dotprod_partial_tile_rows(hip, ta):
     ref = aa[rows] @ b.astype(np.float64)
     bound = 4 * K * np.finfo(np.float32).eps * (np.abs(a).max() * np.abs(b).max())
     np.testing.assert_allclose(got["r"][rows], ref, rtol=0, atol=bound)
+
+
+def test_feeder_offset_zero_matches_the_opencl_oracle(hip):
+    """feeder_offset_zero reproduces the OpenCL write_buffer, which puts a
+    Feeder at offset 0 of its buffer (cl_helper.py:316,326); the MLP's Feeder
+    sits at a non-zero arena offset, so the default differs from it."""
+    ad.reset()
+    a = programs.mlp(steps=3)
+    ad.execute(device=hip(feeder_offset_zero=True))
+    ad.reset()
+    b = programs.mlp(steps=3)
+    ad.execute(device=OracleDevice(feeder_offset_zero=True))
+    assert_params_close(a, b)
+    ad.reset()
+    c = programs.mlp(steps=3)
+    ad.execute(device=OracleDevice())
+    assert any(not np.allclose(x, y) for x, y in zip(a["params"], c["params"]))
+
+
+@pytest.mark.parametrize("R", [5, 6, 1000, 1024])
+def test_exact_reduce_all_elements(hip, R):
+    """exact_reduce: row and column SUM and MAX over every element (the
+    reference's tree drops elements for R = 5, 6, 1000 and pads MAX with 0),
+    against numpy and the oracle's exact mode."""
+    rng = np.random.default_rng(R)
+    a = rng.standard_normal((12, R)).astype(np.float32)
+    neg = -np.abs(a) - 0.5
+    col = rng.standard_normal((R, 12)).astype(np.float32)
+
+    def build(out):
+        Receiver(lambda s, m, cs, cm: out.update(s=s.copy(), m=m.copy(), cs=cs.copy(), cm=cm.copy()),
+                 [Tensor(a).sum(-1), Tensor(neg).max(-1), Tensor(col).sum(0), Tensor(-np.abs(col) - 0.5).max(0)])
+    ad.reset()
+    got = {}
+    build(got)
+    ad.execute(device=hip(exact_reduce=True))
+    ad.reset()
+    ref = {}
+    build(ref)
+    ad.execute(device=OracleDevice(exact_reduce=True))
+    np.testing.assert_allclose(got["s"], a.astype(np.float64).sum(-1), rtol=1e-5, atol=1e-4)
+    np.testing.assert_allclose(got["cs"], col.astype(np.float64).sum(0), rtol=1e-5, atol=1e-4)
+    assert np.array_equal(got["m"], neg.max(-1))
+    assert np.array_equal(got["cm"], (-np.abs(col) - 0.5).max(0))
+    for k in got:
+        np.testing.assert_allclose(got[k].reshape(-1), ref[k].reshape(-1), rtol=1e-5, atol=1e-4)

@@ -192,3 +192,24 @@ def test_lockstep_equals_workitem_when_no_hazard():
     ad.execute(device=OracleDevice(lockstep=False))
     for a, b in zip(out_a["params"], out_b["params"]):
         np.testing.assert_array_equal(a, b)
+
+
+@pytest.mark.parametrize("R", [5, 6, 1000, 1024])
+def test_exact_reduce_mode_sums_every_element(R):
+    """With exact_reduce the oracle combines all R elements: SUM matches a
+    float64 sum and MAX over all-negative rows is the true maximum (the
+    reference's tree drops elements for R = 5, 6, 1000 and pads MAX with 0)."""
+    import ad_amd as ad
+    from ad_amd.graph import Receiver, Tensor
+    from oracle import OracleDevice
+    ad.reset()
+    rng = np.random.default_rng(R)
+    a = rng.standard_normal((7, R)).astype(np.float32)
+    neg = -np.abs(a) - 0.5
+    got = {}
+    Receiver(lambda s, m: got.update(s=s.copy(), m=m.copy()),
+             [Tensor(a).sum(-1), Tensor(neg).max(-1)])
+    ad.execute(device=OracleDevice(exact_reduce=True))
+    np.testing.assert_allclose(got["s"], a.astype(np.float64).sum(-1), rtol=1e-5, atol=1e-4)
+    assert np.array_equal(got["m"], neg.max(-1))
+    ad.reset()
