@@ -12,6 +12,8 @@
 //  * reduce_cols  -- Reduce+Elw, columns contiguous: 64 columns x 4 or 16
 //                    (float4 lanes) row groups per block, coalesced along
 //                    the columns, LDS combine, optional split of the rows.
+//  * pack_bf16, dp_bf16 -- the bf16 DotProd option: operands packed as
+//                    k-contiguous bf16, v_mfma_f32_32x32x16_bf16, fp32 sums.
 // Elementwise (ElwFuse) kernels are emitted whole by the generator.
 #pragma clang fp contract(off)
 
@@ -49,6 +51,85 @@ __device__ __forceinline__ float rop(float a, float b) {
 // elements with float4 loads and stores.
 constexpr int DP_GROUP = 8, DP_CPITCH = 40;
 
+// Block -> output tile.  Workgroups go to the 8 XCDs round-robin, each XCD
+// with its own L2: give every XCD a contiguous run of tiles, ordered in
+// groups of DP_GROUP tile rows, so blocks sharing A rows and B columns share
+// an L2.
+__device__ __forceinline__ void dp_block_tile(int& bx, int& by) {
+  const int gx = gridDim.x, gy = gridDim.y, T = gx * gy;
+  int L = blockIdx.y * gx + blockIdx.x;
+  if (T % 8 == 0) L = (L % 8) * (T / 8) + L / 8;
+  const int per_group = DP_GROUP * gx;
+  const int first = (L / per_group) * DP_GROUP;
+  const int rows = gy - first < DP_GROUP ? gy - first : DP_GROUP;
+  by = first + (L % per_group) % rows;
+  bx = (L % per_group) / rows;
+}
+
+// Epilogue of a DotProd block: the 32x32 accumulator tiles of each wave go
+// through EPI (see the DotProd+Elw notes above); `smem` is the block's LDS,
+// free once the products are done (at least 4 * 32 * DP_CPITCH floats).
+template <int BM, int BN, class EPI>
+__device__ __forceinline__ void dp_epilogue(const EPI& epi, adhip_f32x16 (&acc)[BM / 64][BN / 64], float* smem,
+                                            int m0, int n0, int M, int N, int chunk) {
+  constexpr int TM = BM / 64, TN = BN / 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int lk = lane >> 5, lr = lane & 31;
+  // 32x32 accumulator layout: lane holds column (lane % 32) and rows
+  // 8*(r/4) + 4*(lane/32) + r%4 for r = 0..15.  Per 32x32 tile, the
+  // epilogue's operand loads for all 16 values are issued first, then the
+  // statements run.
+  constexpr int NL = EPI::kLoads > 0 ? EPI::kLoads : 1;
+  if constexpr (EPI::kVec4) {
+    // lane -> row 8*q + lane/8 and columns 4*(lane%8) .. +3 of the tile
+    __syncthreads();
+    float* cs = smem + wave * 32 * DP_CPITCH;
+    const int qr = lane >> 3, qc = 4 * (lane & 7);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int col = n0 + wn * (BN / 2) + j * 32 + qc;
+        const int rbase = m0 + wm * (BM / 2) + i * 32 + qr;
+        float4 lv[4][NL];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (rbase + 8 * q < M && col < N) epi.load4(rbase + 8 * q, col, lv[q]);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) cs[(8 * (r >> 2) + 4 * lk + (r & 3)) * DP_CPITCH + lr] = acc[i][j][r];
+        // lanes read what other lanes of the wave wrote (LDS executes a
+        // wave's operations in order; the fences keep the compiler's order)
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        float4 v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = *reinterpret_cast<const float4*>(cs + (8 * q + qr) * DP_CPITCH + qc);
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (rbase + 8 * q < M && col < N) epi.vec(v[q], rbase + 8 * q, col, chunk, lv[q]);
+      }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        float lv[16][NL];
+        const int col = n0 + wn * (BN / 2) + j * 32 + lr;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+          if (row < M && col < N) epi.load(row, col, lv[r]);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+          if (row < M && col < N) epi(acc[i][j][r], row, col, chunk, lv[r]);
+        }
+      }
+  }
+}
+
 template <int BM, int BN, int SPLIT, int BK, class LA, class LB, class EPI>
 __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& epi, int M, int N, int K) {
   static_assert(BM % 64 == 0 && BN % 64 == 0, "tile must be a multiple of 64");
@@ -83,20 +164,8 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
   const int wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int tiles_m = (M + BM - 1) / BM;
-  int bx = blockIdx.x, by = blockIdx.y;
-  {
-    // Workgroups go to the 8 XCDs round-robin, each XCD with its own L2:
-    // give every XCD a contiguous run of tiles, ordered in groups of
-    // DP_GROUP tile rows, so blocks sharing A rows and B columns share an L2.
-    const int gx = gridDim.x, gy = gridDim.y, T = gx * gy;
-    int L = by * gx + bx;
-    if (T % 8 == 0) L = (L % 8) * (T / 8) + L / 8;
-    const int per_group = DP_GROUP * gx;
-    const int first = (L / per_group) * DP_GROUP;
-    const int rows = gy - first < DP_GROUP ? gy - first : DP_GROUP;
-    by = first + (L % per_group) % rows;
-    bx = (L % per_group) / rows;
-  }
+  int bx, by;
+  dp_block_tile(bx, by);
   const int chunk = SPLIT > 1 ? by / tiles_m : 0;
   const int m0 = (SPLIT > 1 ? by % tiles_m : by) * BM, n0 = bx * BN;
   int kbeg = 0, kend = K;
@@ -256,58 +325,148 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
       cur ^= 1;
     }
   }
-  // 32x32 accumulator layout: lane holds column (lane % 32) and rows
-  // 8*(r/4) + 4*(lane/32) + r%4 for r = 0..15.  Per 32x32 tile, the
-  // epilogue's operand loads for all 16 values are issued first, then the
-  // statements run.
-  constexpr int NL = EPI::kLoads > 0 ? EPI::kLoads : 1;
-  if constexpr (EPI::kVec4) {
-    // lane -> row 8*q + lane/8 and columns 4*(lane%8) .. +3 of the tile
-    __syncthreads();
-    float* cs = smem + wave * 32 * DP_CPITCH;
-    const int qr = lane >> 3, qc = 4 * (lane & 7);
+  dp_epilogue<BM, BN>(epi, acc, smem, m0, n0, M, N, chunk);
+}
+
+// ---------------------------------------------------------------- bf16 DotProd
+// An option, not the reference: operands rounded to bfloat16 (nearest even),
+// products accumulated in fp32 by v_mfma_f32_32x32x16_bf16.
+typedef __bf16 adhip_bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ unsigned adhip_pack2_bf16(float a, float b) {
+  return (unsigned)__builtin_bit_cast(unsigned short, (__bf16)a) |
+         ((unsigned)__builtin_bit_cast(unsigned short, (__bf16)b) << 16);
+}
+
+// pack_bf16<ROLE>: a DotProd operand as a k-contiguous bf16 matrix
+// dst[r * KPAD + k] for r < 64 * gridDim.y, k < 64 * gridDim.x (KPAD), zero
+// outside R x K.  ROLE 0: A, LD::at(r, k); ROLE 1: B, LD::at(k, r).  Each
+// block moves a 64 x 64 tile through LDS: loads coalesced along the
+// operand's contiguous axis, stores of 16 consecutive k per lane.
+template <int ROLE, class LD>
+__device__ __forceinline__ void pack_bf16(const LD& ld, __bf16* __restrict__ dst, int R, int K, int KPAD) {
+  __shared__ float tile[64][65];
+  constexpr bool rows_contig = ROLE == 0 ? LD::kMode == 1 : LD::kMode == 0;
+  const int t = threadIdx.x;
+  const int r0 = blockIdx.y * 64, k0 = blockIdx.x * 64;
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int col = n0 + wn * (BN / 2) + j * 32 + qc;
-        const int rbase = m0 + wm * (BM / 2) + i * 32 + qr;
-        float4 lv[4][NL];
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (rbase + 8 * q < M && col < N) epi.load4(rbase + 8 * q, col, lv[q]);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) cs[(8 * (r >> 2) + 4 * lk + (r & 3)) * DP_CPITCH + lr] = acc[i][j][r];
-        // lanes read what other lanes of the wave wrote (LDS executes a
-        // wave's operations in order; the fences keep the compiler's order)
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-        float4 v[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] = *reinterpret_cast<const float4*>(cs + (8 * q + qr) * DP_CPITCH + qc);
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (rbase + 8 * q < M && col < N) epi.vec(v[q], rbase + 8 * q, col, chunk, lv[q]);
-      }
-  } else {
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        float lv[16][NL];
-        const int col = n0 + wn * (BN / 2) + j * 32 + lr;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
-          if (row < M && col < N) epi.load(row, col, lv[r]);
-        }
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
-          if (row < M && col < N) epi(acc[i][j][r], row, col, chunk, lv[r]);
-        }
-      }
+  for (int i = 0; i < 16; ++i) {
+    int rl, kl;
+    if constexpr (rows_contig) { rl = t & 63; kl = (t >> 6) + 4 * i; }
+    else { kl = t & 63; rl = (t >> 6) + 4 * i; }
+    const int r = r0 + rl, k = k0 + kl;
+    float v = 0.f;
+    if (r < R && k < K) {
+      if constexpr (ROLE == 0) v = ld.at(r, k);
+      else v = ld.at(k, r);
+    }
+    tile[rl][kl] = v;
   }
+  __syncthreads();
+  const int rl = t >> 2, kq = (t & 3) * 16;
+  uint4 w[2];
+  unsigned* u = reinterpret_cast<unsigned*>(w);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) u[j] = adhip_pack2_bf16(tile[rl][kq + 2 * j], tile[rl][kq + 2 * j + 1]);
+  uint4* d = reinterpret_cast<uint4*>(dst + (size_t)(r0 + rl) * KPAD + k0 + kq);
+  d[0] = w[0];
+  d[1] = w[1];
+}
+
+// dp_bf16<BM, BN, SPLIT, BK>: C[m][n] = sum_k A[m][k] * B[n][k] over packed
+// operands (rows padded to the tile, KPAD bf16 per row, zero padded).  K
+// panels of BK in two LDS buffers ([row][k], pitch BK + 8 bf16); per panel,
+// BK/16 MFMA steps of 16 k, a lane taking 8 consecutive k (one 16-byte read)
+// per 32-row tile.  Tile order, K split and epilogue as dp_mfma.
+template <int BM, int BN, int SPLIT, int BK, class EPI>
+__device__ __forceinline__ void dp_bf16(const __bf16* __restrict__ A, const __bf16* __restrict__ B, int KPAD,
+                                        const EPI& epi, int M, int N) {
+  static_assert(BK % 32 == 0, "K panel must be a multiple of 32");
+  constexpr int TM = BM / 64, TN = BN / 64, KP = BK + 8, CH = BK / 8;
+  constexpr int VA = BM * BK / 8 / 256, VB = BN * BK / 8 / 256;   // 16-byte loads per thread
+  static_assert(VA >= 1 && VB >= 1, "tile too small for 256 threads");
+  constexpr int A_HALVES = 2 * BM * KP, B_HALVES = 2 * BN * KP;
+  constexpr int C_FLOATS = EPI::kVec4 ? 4 * 32 * DP_CPITCH : 0;
+  constexpr int S_FLOATS = (A_HALVES + B_HALVES) / 2 > C_FLOATS ? (A_HALVES + B_HALVES) / 2 : C_FLOATS;
+  __shared__ __attribute__((aligned(16))) float smem[S_FLOATS];
+  __bf16* const As = reinterpret_cast<__bf16*>(smem);
+  __bf16* const Bs = As + A_HALVES;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int lk = lane >> 5, lr = lane & 31;
+  const int tiles_m = (M + BM - 1) / BM;
+  int bx, by;
+  dp_block_tile(bx, by);
+  const int chunk = SPLIT > 1 ? by / tiles_m : 0;
+  const int m0 = (SPLIT > 1 ? by % tiles_m : by) * BM, n0 = bx * BN;
+  int kbeg = 0, kend = KPAD;
+  if constexpr (SPLIT > 1) {
+    const int kc = ((KPAD + SPLIT - 1) / SPLIT + BK - 1) / BK * BK;
+    kbeg = chunk * kc;
+    kend = kbeg + kc < KPAD ? kbeg + kc : KPAD;
+  }
+  uint4 ra[VA], rb[VB];
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < VA; ++i) {
+      const int v = tid + 256 * i;
+      ra[i] = *reinterpret_cast<const uint4*>(A + (size_t)(m0 + v / CH) * KPAD + k0 + 8 * (v % CH));
+    }
+#pragma unroll
+    for (int i = 0; i < VB; ++i) {
+      const int v = tid + 256 * i;
+      rb[i] = *reinterpret_cast<const uint4*>(B + (size_t)(n0 + v / CH) * KPAD + k0 + 8 * (v % CH));
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < VA; ++i) {
+      const int v = tid + 256 * i;
+      *reinterpret_cast<uint4*>(As + (buf * BM + v / CH) * KP + 8 * (v % CH)) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < VB; ++i) {
+      const int v = tid + 256 * i;
+      *reinterpret_cast<uint4*>(Bs + (buf * BN + v / CH) * KP + 8 * (v % CH)) = rb[i];
+    }
+  };
+  adhip_f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  if (kbeg < kend) {
+    load(kbeg);
+    store(0);
+    __syncthreads();
+    int cur = 0;
+    for (int k0 = kbeg; k0 < kend; k0 += BK) {
+      const bool more = k0 + BK < kend;
+      if (more) load(k0 + BK);
+#pragma unroll
+      for (int st = 0; st < BK / 16; ++st) {
+        adhip_bf16x8 af[TM], bf[TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          af[i] = *reinterpret_cast<const adhip_bf16x8*>(As + (cur * BM + wm * (BM / 2) + i * 32 + lr) * KP + 16 * st + 8 * lk);
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          bf[j] = *reinterpret_cast<const adhip_bf16x8*>(Bs + (cur * BN + wn * (BN / 2) + j * 32 + lr) * KP + 16 * st + 8 * lk);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+      }
+      if (more) store(cur ^ 1);
+      __syncthreads();
+      cur ^= 1;
+    }
+  }
+  dp_epilogue<BM, BN>(epi, acc, smem, m0, n0, M, N, chunk);
 }
 
 // ---------------------------------------------------------------- Reduce+Elw

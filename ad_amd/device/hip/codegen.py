@@ -406,6 +406,19 @@ HOIST_MAX = 8
 _NO_SIZES = BufferInfo()
 
 
+@dataclass(frozen=True)
+class PlanOptions:
+    """Choices that change results, all off by default (the reference's):
+    ``exact_reduce`` -- reductions combine every element (``kept_elements``);
+    ``dot`` -- "bf16" rounds DotProd operands to bfloat16 and sums in fp32 on
+    bf16 MFMA (``pack_plan``, ``dotprod_bf16_plan``)."""
+    exact_reduce: bool = False
+    dot: str = "fp32"
+
+
+DEFAULT_OPTIONS = PlanOptions()
+
+
 class _StoreTracker:
     """The regions one element has stored to so far, and the operand reads
     hoisted ahead of every store (``_l[k]``, up to ``limit`` of them)."""
@@ -962,6 +975,51 @@ def epilogue_vec_ok(stmts, M, N) -> bool:
     return _vector_plan([st for st in stmts if st[0] != "init"], M * N, "dp", N)
 
 
+def _dp_epi_struct(stmts, params: Params, ity, M, N, partial_off=None) -> str:
+    """The ``EPI`` functor of a DotProd kernel: the epilogue statements on
+    the product (four consecutive columns per call with float4 accesses when
+    every access allows it, else one element per call), or the store of a
+    partial product to scratch at ``partial_off`` ([chunk][M][N])."""
+    gid = f"const {ity} _global_id = _x * ({ity}){N} + _y; (void)_global_id;"
+    if partial_off is not None:
+        assert not stmts, "a DotProd storing partial products runs no epilogue"
+    vec4 = N % 4 == 0 and (partial_off is not None or epilogue_vec_ok(stmts, M, N))
+    if vec4:
+        if partial_off is not None:
+            pp = params.ptr("scratch", 0, partial_off)
+            lines, loads = [f"*reinterpret_cast<float4*>({pp} + ((unsigned long long)_chunk * {M}ull + _x) * "
+                            f"{N}ull + _y) = _value;"], []
+        else:
+            tracker = _StoreTracker(VEC_HOIST_MAX)
+            lines = _vector_lines(stmts, ity, params, "dp", hoist=tracker)
+            loads = tracker.loads
+        body = "\n    ".join(lines)
+        fill = "".join(f"\n    _l[{i}] = {e};" for i, e in enumerate(loads))
+        return (f"struct EPI {{ @FIELDS@\n"
+                f"  static constexpr bool kVec4 = true;\n"
+                f"  static constexpr int kLoads = {len(loads)};\n"
+                f"  __device__ void load4({ity} _x, {ity} _y, float4* _l) const {{\n"
+                f"    {gid} (void)_l;{fill}\n  }}\n"
+                f"  __device__ void vec(float4 _value, {ity} _x, {ity} _y, int _chunk, const float4* _l) const {{\n"
+                f"    {gid} (void)_chunk; (void)_l;\n    {body}\n  }} }};\n")
+    loads = []
+    if partial_off is not None:
+        pp = params.ptr("scratch", 0, partial_off)
+        body = (f"{pp}[((unsigned long long)_chunk * {M}ull + _x) * {N}ull + _y] = _value;")
+    else:
+        low = Lowerer(ity, params, hoist=True)
+        body = "\n    ".join(low.statements(stmts, "_value"))
+        loads = low.loads
+    fill = "".join(f"\n    _l[{i}] = {e};" for i, e in enumerate(loads))
+    return (f"struct EPI {{ @FIELDS@\n"
+            f"  static constexpr bool kVec4 = false;\n"
+            f"  static constexpr int kLoads = {len(loads)};\n"
+            f"  __device__ void load({ity} _x, {ity} _y, float* _l) const {{\n"
+            f"    {gid} (void)_l;{fill}\n  }}\n"
+            f"  __device__ void operator()(float _value, {ity} _x, {ity} _y, int _chunk, const float* _l) const {{\n"
+            f"    {gid} (void)_chunk; (void)_l;\n    {body}\n  }} }};\n")
+
+
 def dotprod_plan(stmts, dp, A=None, B=None, config=None, partial_off=None) -> KernelPlan:
     """DotProd (+ elementwise epilogue) on fp32 MFMA tiles
     (kernels/dotprod.py:7-43, dp_elw_fuse.py:26-65 semantics).  ``A``/``B``
@@ -979,50 +1037,71 @@ def dotprod_plan(stmts, dp, A=None, B=None, config=None, partial_off=None) -> Ke
     params = Params()
     la, _ = _loader_struct("LA", A, "A", params, ity, (M, K))
     lb, _ = _loader_struct("LB", B, "B", params, ity, (K, N))
-    gid = f"const {ity} _global_id = _x * ({ity}){N} + _y; (void)_global_id;"
-    if partial_off is not None:
-        assert not stmts, "a DotProd storing partial products runs no epilogue"
-    vec4 = N % 4 == 0 and (partial_off is not None or epilogue_vec_ok(stmts, M, N))
-    if vec4:
-        # four consecutive columns per call, float4 loads and stores
-        if partial_off is not None:
-            pp = params.ptr("scratch", 0, partial_off)
-            lines, loads = [f"*reinterpret_cast<float4*>({pp} + ((unsigned long long)_chunk * {M}ull + _x) * "
-                            f"{N}ull + _y) = _value;"], []
-        else:
-            tracker = _StoreTracker(VEC_HOIST_MAX)
-            lines = _vector_lines(stmts, ity, params, "dp", hoist=tracker)
-            loads = tracker.loads
-        body = "\n    ".join(lines)
-        fill = "".join(f"\n    _l[{i}] = {e};" for i, e in enumerate(loads))
-        epi = (f"struct EPI {{ @FIELDS@\n"
-               f"  static constexpr bool kVec4 = true;\n"
-               f"  static constexpr int kLoads = {len(loads)};\n"
-               f"  __device__ void load4({ity} _x, {ity} _y, float4* _l) const {{\n"
-               f"    {gid} (void)_l;{fill}\n  }}\n"
-               f"  __device__ void vec(float4 _value, {ity} _x, {ity} _y, int _chunk, const float4* _l) const {{\n"
-               f"    {gid} (void)_chunk; (void)_l;\n    {body}\n  }} }};\n")
-    else:
-        loads = []
-        if partial_off is not None:
-            pp = params.ptr("scratch", 0, partial_off)
-            body = (f"{pp}[((unsigned long long)_chunk * {M}ull + _x) * {N}ull + _y] = _value;")
-        else:
-            low = Lowerer(ity, params, hoist=True)
-            body = "\n    ".join(low.statements(stmts, "_value"))
-            loads = low.loads
-        fill = "".join(f"\n    _l[{i}] = {e};" for i, e in enumerate(loads))
-        epi = (f"struct EPI {{ @FIELDS@\n"
-               f"  static constexpr bool kVec4 = false;\n"
-               f"  static constexpr int kLoads = {len(loads)};\n"
-               f"  __device__ void load({ity} _x, {ity} _y, float* _l) const {{\n"
-               f"    {gid} (void)_l;{fill}\n  }}\n"
-               f"  __device__ void operator()(float _value, {ity} _x, {ity} _y, int _chunk, const float* _l) const {{\n"
-               f"    {gid} (void)_chunk; (void)_l;\n    {body}\n  }} }};\n")
+    epi = _dp_epi_struct(stmts, params, ity, M, N, partial_off)
     init = _init_list(params)
     src = ((la + lb + epi).replace("@FIELDS@", _fields(params)) +
            f"extern \"C\" __global__ void __launch_bounds__(256) {KNAME}({_params_decl(params)}) {{\n"
            f"  adhip::dp_mfma<{BM}, {BN}, {split}, {BK}>(LA{{{init}}}, LB{{{init}}}, EPI{{{init}}}, {M}, {N}, {K});\n}}\n")
+    grid = (ceil(N / BN), ceil(M / BM) * split, 1)
+    return KernelPlan(src, grid, (256, 1, 1), _plan_args(params), family="dotprod",
+                      flops=2 * M * N * K)
+
+
+# ------------------------------------------------------------------ bf16 DotProd option
+BF16_K_ALIGN = 64
+
+
+def bf16_dims(M, N, K, config):
+    """Padded sizes of the packed bf16 operands: rows to the block tile, K to
+    a multiple of 64 (the pack tile)."""
+    BM, BN = config[0], config[1]
+    return ceil(M / BM) * BM, ceil(N / BN) * BN, ceil(K / BF16_K_ALIGN) * BF16_K_ALIGN
+
+
+# depth of the bf16 K panels (64 measured no faster at 4096^3 and slower on
+# the C5 step)
+BF16_PANEL = 32
+
+
+def pack_plan(karg, role, rows, K, rows_pad, k_pad, dst_off, dims) -> KernelPlan:
+    """``scratch[dst_off]`` as bf16 ``[rows_pad][k_pad]``: the DotProd operand
+    ``karg`` (``role`` "A": element (r, k) is A(r, k); "B": B(k, r)) rounded
+    to bf16, k-contiguous, zero padded."""
+    bound = _expr_bound([("copy", _Stmt([karg], _scratch_km(0, Global())))], 0,
+                        max(rows_pad, k_pad), max(rows_pad, k_pad))
+    ity = _ity(bound)
+    params = Params()
+    ld, _ = _loader_struct("LD", karg, role, params, ity, dims)
+    dst = params.ptr("scratch", 0, dst_off)
+    init = _init_list(params)
+    src = (ld.replace("@FIELDS@", _fields(params)) +
+           f"extern \"C\" __global__ void __launch_bounds__(256) {KNAME}({_params_decl(params)}) {{\n"
+           f"  adhip::pack_bf16<{0 if role == 'A' else 1}>(LD{{{init}}}, reinterpret_cast<__bf16*>({dst}), "
+           f"{rows}, {K}, {k_pad});\n}}\n")
+    grid = (k_pad // 64, rows_pad // 64, 1)
+    return KernelPlan(src, grid, (256, 1, 1), _plan_args(params), family="pack",
+                      bytes=4 * rows * K + 2 * rows_pad * k_pad)
+
+
+def dotprod_bf16_plan(stmts, dp, a_off, b_off, config, partial_off=None) -> KernelPlan:
+    """DotProd (+ epilogue) over operands packed by ``pack_plan`` at scratch
+    ``a_off`` / ``b_off``, on bf16 MFMA with fp32 sums; otherwise as
+    ``dotprod_plan``."""
+    M, N = dp.shape
+    K = dp.children_shapes[0][1]
+    BM, BN, split = config[0], config[1], config[2]
+    _, _, k_pad = bf16_dims(M, N, K, config)
+    bound = _expr_bound(stmts, M * N, max(M, K), max(N, K))
+    ity = _ity(bound)
+    params = Params()
+    pa = params.ptr("scratch", 0, a_off)
+    pb = params.ptr("scratch", 0, b_off)
+    epi = _dp_epi_struct(stmts, params, ity, M, N, partial_off)
+    init = _init_list(params)
+    src = (epi.replace("@FIELDS@", _fields(params)) +
+           f"extern \"C\" __global__ void __launch_bounds__(256) {KNAME}({_params_decl(params)}) {{\n"
+           f"  adhip::dp_bf16<{BM}, {BN}, {split}, {BF16_PANEL}>(reinterpret_cast<const __bf16*>({pa}), "
+           f"reinterpret_cast<const __bf16*>({pb}), {k_pad}, EPI{{{init}}}, {M}, {N});\n}}\n")
     grid = (ceil(N / BN), ceil(M / BM) * split, 1)
     return KernelPlan(src, grid, (256, 1, 1), _plan_args(params), family="dotprod",
                       flops=2 * M * N * K)
@@ -1157,7 +1236,7 @@ def reduce_plan(stmts, red, partial_off=None, exact=False) -> KernelPlan:
 
 
 # ------------------------------------------------------------------ lockstep fallback
-def lockstep_plans(stmts, n, index_kind, n_cols, init_node, scratch_base, exact=False):
+def lockstep_plans(stmts, n, index_kind, n_cols, init_node, scratch_base, opts=DEFAULT_OPTIONS):
     """Exact lockstep semantics for a command with cross-element memory
     dependences: one kernel per statement, each computing its value for every
     element into a staging array before a second kernel stores it.  Temps and
@@ -1171,7 +1250,7 @@ def lockstep_plans(stmts, n, index_kind, n_cols, init_node, scratch_base, exact=
     plans = []
     if init_node is not None:
         sink = _scratch_km(init_off, _identity_access(index_kind, n_cols))
-        plans.extend(first_pass_plans([("init", _ValueSink(sink))], n, init_node, alloc, exact))
+        plans.extend(first_pass_plans([("init", _ValueSink(sink))], n, init_node, alloc, opts))
     for kind, node in stmts:
         if kind == "tmp":
             continue
@@ -1244,10 +1323,9 @@ def _stmt_plan(kind, node, n, index_kind, n_cols, temp_off, stage_off, init_off,
 
 
 # ------------------------------------------------------------------ per-command entry
-def command_plans(cmd, buffers: BufferInfo, scratch_base: int, exact_reduce: bool = False):
-    """Plans for one Proc command and the scratch floats they need.  With
-    ``exact_reduce`` every reduction combines all of its elements (see
-    ``kept_elements``)."""
+def command_plans(cmd, buffers: BufferInfo, scratch_base: int, opts: PlanOptions = DEFAULT_OPTIONS):
+    """Plans for one Proc command and the scratch floats they need, under
+    ``opts``."""
     if isinstance(cmd, (BinaryNode, UnaryNode, ContigiousNode)):
         stmts, n, kind, cols, init = statements([cmd]), prod(cmd.shape), "global", 1, None
     elif isinstance(cmd, ElwFuse):
@@ -1272,9 +1350,9 @@ def command_plans(cmd, buffers: BufferInfo, scratch_base: int, exact_reduce: boo
     for group in groups:
         pairs = conflict_pairs(group, buffers, kind, cols)
         if any(i == j for i, j in pairs):
-            ps, need = lockstep_plans(group, n, kind, cols, init, end, exact_reduce)
+            ps, need = lockstep_plans(group, n, kind, cols, init, end, opts)
         else:
-            ps, need = phased_plans(group, pairs, n, kind, cols, init, end, exact_reduce)
+            ps, need = phased_plans(group, pairs, n, kind, cols, init, end, opts)
         reads, writes = stmt_regions(group, buffers) if len(groups) > 1 else (None, None)
         for p in ps:
             p.reads, p.writes = reads, writes
@@ -1346,17 +1424,32 @@ def epilogue_loads(part):
     return len(seen)
 
 
-def first_pass_plans(part, n, init_node, alloc: ScratchAlloc, exact=False):
+def first_pass_plans(part, n, init_node, alloc: ScratchAlloc, opts=DEFAULT_OPTIONS):
     """Plans of the pass that runs the DotProd or Reduce of a command with
     ``part`` as its epilogue: operand gathers, then the product (or the
     reduction) with the epilogue in registers, or -- split over K / rows --
     partial results followed by an elementwise pass that combines them in
     chunk order and runs the epilogue."""
+    exact = opts.exact_reduce
     if isinstance(init_node, DotProdNode):
         M, N = init_node.shape
         K = init_node.children_shapes[0][1]
         cfg = dp_config(M, N, K)
         A, B = init_node.kargs
+        if opts.dot == "bf16":
+            # both operands packed to k-contiguous bf16 in scratch, then the product
+            m_pad, n_pad, k_pad = bf16_dims(M, N, K, cfg)
+            a_off = alloc.take((m_pad * k_pad + 1) // 2)
+            b_off = alloc.take((n_pad * k_pad + 1) // 2)
+            pre = [pack_plan(A, "A", M, K, m_pad, k_pad, a_off, (M, K)),
+                   pack_plan(B, "B", N, K, n_pad, k_pad, b_off, (K, N))]
+            if cfg[2] == 1 and epilogue_loads(part) <= EPILOGUE_MAX_LOADS:
+                return pre + [dotprod_bf16_plan(part, init_node, a_off, b_off, cfg)]
+            poff = alloc.take(cfg[2] * M * N)
+            main = dotprod_bf16_plan([], init_node, a_off, b_off, cfg, partial_off=poff)
+            comb = elementwise_plan([("sum", (poff, cfg[2], M * N, 0, False))] + part, M * N,
+                                    index_kind="dp", n_cols=N, init_value="_value")
+            return pre + [main, comb]
         pre = []
         if isinstance(A, KConcat) and M * N * K >= GATHER_MIN_MACS:
             off = alloc.take(M * K)
@@ -1421,7 +1514,7 @@ def _temp_uses(stmts):
     return reads, assigns
 
 
-def phased_plans(stmts, pairs, n, index_kind, n_cols, init_node, scratch_base=0, exact=False):
+def phased_plans(stmts, pairs, n, index_kind, n_cols, init_node, scratch_base=0, opts=DEFAULT_OPTIONS):
     """A command whose statements conflict across elements, run as several
     passes over the elements (one kernel each): the first pass is the
     DotProd/Reduce (if any) with the statements up to the first conflict in
@@ -1464,7 +1557,7 @@ def phased_plans(stmts, pairs, n, index_kind, n_cols, init_node, scratch_base=0,
         tail = [("store", (tid, slot[tid])) for tid in sorted(slot) if assigned_in[tid] == pi]
         part = head + body + tail
         if pi == 0 and init_node is not None:
-            plans.extend(first_pass_plans(part, n, init_node, alloc, exact))
+            plans.extend(first_pass_plans(part, n, init_node, alloc, opts))
         else:
             kind = "global" if init_node is None else ("dp" if isinstance(init_node, DotProdNode) else "red")
             plans.append(elementwise_plan(part, n, index_kind=kind, n_cols=n_cols))

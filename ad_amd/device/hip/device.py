@@ -73,7 +73,7 @@ class HIPDevice(Device):
     def __init__(self, device_index: int = 0, use_graphs: bool = True, jit_threads: int = None,
                  group_launches: bool = True, lanes: int = 1, receiver_lag: int = 0,
                  exact_reduce: bool = False, feeder_offset_zero: bool = False,
-                 strict_temps: bool = False):
+                 strict_temps: bool = False, dot_precision: str = "fp32"):
         super().__init__()
         # fixes of reference behaviours, off by default (the reference's results):
         # exact_reduce: reductions combine all R elements (the reference's
@@ -85,7 +85,12 @@ class HIPDevice(Device):
         # strict_temps: raise on a fused temp read through a non-identity
         #   access, which the reference silently reads as the element's own
         #   value (karg.py:47-48).
+        # dot_precision "bf16" (beyond the reference, which computes in fp32):
+        #   DotProd operands rounded to bfloat16, products summed in fp32 on
+        #   bf16 MFMA.
+        assert dot_precision in ("fp32", "bf16"), "dot_precision must be fp32 or bf16"
         self.exact_reduce = exact_reduce
+        self._plan_opts = codegen.PlanOptions(exact_reduce=exact_reduce, dot=dot_precision)
         self.feeder_offset_zero = feeder_offset_zero
         self.strict_temps = strict_temps
         # Receivers inside a replayed loop: their callbacks run this many
@@ -190,7 +195,7 @@ class HIPDevice(Device):
         for cmd in self._pending:
             if self.strict_temps:
                 self._check_temps(cmd)
-            ps, need, multipass = codegen.command_plans(cmd, info, 0, self.exact_reduce)
+            ps, need, multipass = codegen.command_plans(cmd, info, 0, self._plan_opts)
             plans[cmd.program_id] = ps
             needs[cmd.program_id] = (need + 63) // 64 * 64
             regions[cmd.program_id] = codegen.command_regions(cmd, info)

@@ -18,7 +18,9 @@
 * ``other_configs``: C1 (the MLP of examples/linear.py, a Feeder upload per
   step), C3 (LayerNorm fwd+bwd at [16384,1024], GB/s over the Proc's
   per-command bytes and over the 5-pass HBM floor) and C4 (1-layer
-  transformer) at full size, graph-replayed.
+  transformer) at full size, graph-replayed; and the bf16 DotProd option
+  (beyond the reference): the 4096^3 DotProd+Elw and the C5 step with
+  DotProd operands rounded to bf16.
 * ``cpu_baseline``: the CPU restatement of the reference OpenCL backend
   (``oracle``, one OpenMP iteration per work-item, sequential k-loops) timed
   on this host on a bounded sample of the same workload (the step's FFN
@@ -40,6 +42,7 @@ if ROOT not in sys.path:
 METRIC = "transformer train steps/s; fused DotProd TFLOP/s + ElwFuse GB/s vs MI355X peak"
 PEAK_FP32_MFMA_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
+PEAK_BF16_MFMA_TFLOPS = 2500.0
 
 
 def log(msg):
@@ -81,19 +84,21 @@ def _time_launches(dev, cmds, reps, warmup=2):
     return dev.ctx.elapsed_ms(10, 11) / reps
 
 
-def micro_dotprod(reps):
+def micro_dotprod(reps, dot="fp32"):
+    """The 4096^3 DotProd+Elw command; with ``dot="bf16"`` its time includes
+    the two operand-packing kernels."""
     import ad_amd as ad
     from ad_amd import workloads
     from ad_amd.device.hip import HIPDevice
     ad.reset()
     workloads.dotprod_elw(4096, 4096, 4096)
     proc = ad.compile_proc()
-    dev = HIPDevice()
+    dev = HIPDevice(dot_precision=dot)
     dev.prepare(proc)
     cmds = _commands(proc)
     assert len(cmds) == 1, [type(c).__name__ for c in cmds]
-    plan = dev.kernels[cmds[0].program_id]
-    assert len(plan) == 1 and plan[0].family == "dotprod"
+    plan = [p for p in dev.kernels[cmds[0].program_id] if p.family == "dotprod"]
+    assert len(plan) == 1
     ms = _time_launches(dev, cmds, reps)
     flops = 2 * 4096 ** 3
     dev.close()
@@ -149,7 +154,7 @@ def micro_elw(reps, copies=2):
     return {"kernel": name, "ms": ms, "bytes": nbytes, "gbs": nbytes / ms / 1e6}
 
 
-def transformer_steps(config, steps, warmup, eager=False, lanes=1):
+def transformer_steps(config, steps, warmup, eager=False, lanes=1, dot="fp32"):
     import ad_amd as ad
     from ad_amd import workloads
     from ad_amd.device.hip import HIPDevice
@@ -162,7 +167,7 @@ def transformer_steps(config, steps, warmup, eager=False, lanes=1):
     t1 = time.perf_counter()
     step_flops = workloads.dotprod_flops(proc)
     log(f"{config}: traced + compiled in {t1 - t0:.1f} s; {step_flops / 1e12:.3f} TFLOP of DotProd per step")
-    dev = HIPDevice(use_graphs=not eager, lanes=lanes)
+    dev = HIPDevice(use_graphs=not eager, lanes=lanes, dot_precision=dot)
     dev.prepare(proc)
     t2 = time.perf_counter()
     log(f"{config}: device init + JIT in {t2 - t1:.1f} s; {dev.stats}")
@@ -252,6 +257,15 @@ def other_configs():
                              "step_dotprod_tflops": round(c4["step_flops"] / (ms * 1e9), 2),
                              "launches_per_step": c4["launches_per_step"]}
     log(f"c4: {ms:.2f} ms/step, {1e3 / ms:.1f} steps/s")
+    dp = micro_dotprod(10, dot="bf16")
+    c5 = transformer_steps("c5", 20, 3, dot="bf16")
+    ms = c5["event_ms"] / 20
+    out["bf16_dotprod"] = {
+        "note": "option beyond the reference (fp32): DotProd operands rounded to bf16, fp32 sums",
+        "dotprod_elw_4096_tflops": round(dp["tflops"], 1),
+        "dotprod_elw_4096_frac_of_bf16_peak": round(dp["tflops"] / PEAK_BF16_MFMA_TFLOPS, 4),
+        "c5_steps_per_s": round(1e3 / ms, 2), "c5_ms_per_step": round(ms, 3)}
+    log(f"bf16 DotProds: 4096^3 {dp['tflops']:.1f} TFLOP/s (packing included); c5 {1e3 / ms:.1f} steps/s")
     return out
 
 

@@ -362,3 +362,41 @@ def test_exact_reduce_all_elements(hip, R):
     assert np.array_equal(got["cm"], (-np.abs(col) - 0.5).max(0))
     for k in got:
         np.testing.assert_allclose(got[k].reshape(-1), ref[k].reshape(-1), rtol=1e-5, atol=1e-4)
+
+
+@pytest.mark.parametrize("M,K,N", [(256, 512, 128), (300, 200, 130), (1, 3, 1), (130, 70, 257), (64, 4096, 64)])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, True)])
+def test_bf16_dotprod_bound(hip, M, K, N, ta, tb):
+    """dot_precision="bf16" (beyond the reference): operands rounded to
+    bfloat16 (unit roundoff 2^-8), products exact in fp32, fp32 sums.  Each
+    output obeys |C - A@B| <= (2^-7 + 2^-15 + K 2^-23) (|A| @ |B|), against
+    float64; the epilogue (+bias) runs on the product as in fp32."""
+    rng = np.random.default_rng(M * 13 + K * 5 + N)
+    a = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    b = rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    bias = rng.standard_normal((N,)).astype(np.float32)
+    r = ((Tensor(a).T() if ta else Tensor(a)) @ (Tensor(b).T() if tb else Tensor(b))) + Tensor(bias)
+    got = {}
+    Receiver(lambda v: got.setdefault("r", v.copy()), [r])
+    ad.execute(device=hip(dot_precision="bf16"))
+    aa = (a.T if ta else a).astype(np.float64)
+    bb = (b.T if tb else b).astype(np.float64)
+    ref = aa @ bb + bias
+    bound = (2.0 ** -7 + 2.0 ** -15 + K * 2.0 ** -23) * (np.abs(aa) @ np.abs(bb)) + 1e-6
+    err = np.abs(got["r"] - ref)
+    assert np.all(err <= bound), float((err / bound).max())
+    if K > 16:
+        # the rounding is really there: fp32 operands would be far closer
+        assert err.max() > 1e-4 * np.abs(ref).max()
+
+
+def test_bf16_training_steps(hip):
+    """A transformer trained for 3 steps with bf16 DotProds stays close to
+    the fp32 oracle (parameters move by lr * grad; the bf16 gradients differ
+    by about 1 %)."""
+    from ad_amd import workloads
+    a, b = run_both(lambda: workloads.transformer(layers=1, d_model=64, heads=4, ff=128, seq=16, batch=2,
+                                                  steps=3), lambda: hip(dot_precision="bf16"))
+    for x, y in zip(a["params"], b["params"]):
+        assert np.all(np.isfinite(x))
+        np.testing.assert_allclose(x, y, rtol=0, atol=2e-3)
