@@ -671,9 +671,12 @@ def _vector_plan(stmts, n, index_kind="global", n_cols=1):
     for kind, node in stmts:
         if kind in ("tmp", "load", "store", "sum"):
             continue
-        for k in node.kargs:
-            if not _vec_operand_ok(k, index_kind):
-                return False
+        # an init statement's value is the product or reduction (never its
+        # operands, which are read in their own kernel)
+        if kind != "init":
+            for k in node.kargs:
+                if not _vec_operand_ok(k, index_kind):
+                    return False
         if not node.kres.is_temp and not _vec_access_ok(node.kres, index_kind, True):
             return False
     return True
@@ -967,12 +970,7 @@ def epilogue_vec_ok(stmts, M, N) -> bool:
     consecutive columns: every access it makes (the product's own store
     included) is contiguous and 4-aligned along the row, or constant over
     the group."""
-    if N % 4 != 0 or not stmts:
-        return False
-    for kind, node in stmts:
-        if kind == "init" and not node.kres.is_temp and not _vec_access_ok(node.kres, "dp", True):
-            return False
-    return _vector_plan([st for st in stmts if st[0] != "init"], M * N, "dp", N)
+    return N % 4 == 0 and bool(stmts) and _vector_plan(stmts, M * N, "dp", N)
 
 
 def _dp_epi_struct(stmts, params: Params, ity, M, N, partial_off=None) -> str:
