@@ -474,7 +474,7 @@ __device__ __forceinline__ void dp_bf16(const __bf16* __restrict__ A, const __bf
 // LD::inc(y) is false for elements the reference's work-group tree drops.
 //
 // reduce_rows: waves stride over the rows (a bounded grid keeps every wave
-// busy across several rows); per row, each lane keeps up to eight float4
+// busy across several rows); per row, each lane keeps up to sixteen float4
 // loads in flight, then a butterfly over the wave; lane 0 runs the epilogue.
 template <int OP, class LD, class EPI>
 __device__ __forceinline__ void reduce_rows(const LD& ld, const EPI& epi, unsigned V, unsigned R,
@@ -488,18 +488,16 @@ __device__ __forceinline__ void reduce_rows(const LD& ld, const EPI& epi, unsign
       float a[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) a[u] = id;
-      unsigned y = lane * 4;
-      for (; y + 7 * 256 < R; y += 8 * 256) {
-        float4 v[8];
+      // 16 float4 loads in flight per lane; the last round is predicated
+      // (identity for the loads past the row)
+      const float4 idv = make_float4(id, id, id, id);
+      for (unsigned y0 = lane * 4; y0 < R; y0 += 16 * 256) {
+        float4 v[16];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = ld.at4(row, y + u * 256);
+        for (int u = 0; u < 16; ++u) v[u] = y0 + u * 256 < R ? ld.at4(row, y0 + u * 256) : idv;
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-          a[u] = rop<OP>(rop<OP>(rop<OP>(rop<OP>(a[u], v[u].x), v[u].y), v[u].z), v[u].w);
-      }
-      for (; y < R; y += 256) {
-        const float4 v0 = ld.at4(row, y);
-        a[0] = rop<OP>(rop<OP>(rop<OP>(rop<OP>(a[0], v0.x), v0.y), v0.z), v0.w);
+        for (int u = 0; u < 16; ++u)
+          a[u & 7] = rop<OP>(rop<OP>(rop<OP>(rop<OP>(a[u & 7], v[u].x), v[u].y), v[u].z), v[u].w);
       }
       acc = rop<OP>(rop<OP>(rop<OP>(a[0], a[1]), rop<OP>(a[2], a[3])),
                     rop<OP>(rop<OP>(a[4], a[5]), rop<OP>(a[6], a[7])));
