@@ -47,6 +47,7 @@ from .schedule import assign_lanes, schedule_dag
 
 ALIGN = 256
 SCRATCH_RING_FLOATS = 64 << 20     # 256 MiB of scratch slots for multi-pass commands
+UNROLL_LAUNCHES = 256              # kernel commands per unrolled loop graph, at most
 _code_cache = {}            # source text -> code object (process-wide)
 _code_lock = threading.Lock()
 
@@ -73,7 +74,7 @@ class HIPDevice(Device):
     def __init__(self, device_index: int = 0, use_graphs: bool = True, jit_threads: int = None,
                  group_launches: bool = True, lanes: int = 1, receiver_lag: int = 0,
                  exact_reduce: bool = False, feeder_offset_zero: bool = False,
-                 strict_temps: bool = False, dot_precision: str = "fp32"):
+                 strict_temps: bool = False, dot_precision: str = "fp32", loop_unroll: int = 32):
         super().__init__()
         # fixes of reference behaviours, off by default (the reference's results):
         # exact_reduce: reductions combine all R elements (the reference's
@@ -90,6 +91,11 @@ class HIPDevice(Device):
         #   bf16 MFMA.
         assert dot_precision in ("fp32", "bf16"), "dot_precision must be fp32 or bf16"
         self.exact_reduce = exact_reduce
+        # a replayed loop body without Receivers is also captured as a graph of
+        # up to `loop_unroll` consecutive iterations (bounded by UNROLL_LAUNCHES
+        # kernel commands per graph), so short bodies pay one graph launch and
+        # one staging round per several iterations
+        self.loop_unroll = max(1, loop_unroll)
         self._plan_opts = codegen.PlanOptions(exact_reduce=exact_reduce, dot=dot_precision)
         self.feeder_offset_zero = feeder_offset_zero
         self.strict_temps = strict_temps
@@ -117,11 +123,14 @@ class HIPDevice(Device):
         self._allocs = []
         self._contents = {}
         self._pending = []
-        self._feeder_slots = {}      # feeder id -> staging byte offset
+        self._feeder_slots = {}      # feeder id -> staging byte offsets, [parity * unroll + u]
+        self._feeder_loop = {}       # feeder id -> ForNode id of its loop body
+        self._unroll = {}            # ForNode id -> iterations per unrolled graph
         self._recv_slots = {}        # in-loop receiver id -> (slot byte offset per parity, bytes)
-        self._graphs = {}            # ForNode id -> ([graph per slot parity], feeders, receivers)
-        self._iteration = {}         # ForNode id -> iterations replayed so far
+        self._graphs = {}            # ForNode id -> ([single-iteration graph per parity], [unrolled graph per parity] or None, feeders, receivers)
+        self._launches = {}          # ForNode id -> graph launches so far
         self._parity = 0
+        self._slot = 0
         self._schedules = {}         # Proc id -> one-lane items (captured into graphs)
         self._lane_schedules = {}    # Proc id -> items over self.lanes lanes (uncaptured runs)
         self._capturing = False
@@ -167,12 +176,24 @@ class HIPDevice(Device):
 
     def _finish_init(self, proc):
         off, info = self._layout()
-        # two staging slots per Feeder: a replayed loop fills one while the
-        # graph of the previous iteration reads the other
+        for loop in self._all_loops(proc):
+            body = loop.get_proc()
+            n_cmds = sum(1 for c in body.procedure if isinstance(c, (Node, FuseBase))
+                         and not isinstance(c, (Feeder, Receiver, ForNode)))
+            has_recv = any(isinstance(c, Receiver) for c in body.procedure)
+            self._unroll[loop.id] = 1 if has_recv or not self._capturable(body) else \
+                max(1, min(self.loop_unroll, UNROLL_LAUNCHES // max(1, n_cmds)))
+            for c in body.procedure:
+                if isinstance(c, Feeder):
+                    self._feeder_loop[c.id] = loop.id
+        # two sets of staging slots per Feeder (one per iteration of an
+        # unrolled graph): a replayed loop fills one set while the graph of
+        # the previous launch reads the other
         for fid in list(self._feeder_slots):
             size = _align(self._feeder_size.get(fid, 0) * 4)
-            self._feeder_slots[fid] = (off, off + size)
-            off += 2 * size
+            count = 2 * self._unroll.get(self._feeder_loop.get(fid), 1)
+            self._feeder_slots[fid] = [off + i * size for i in range(count)]
+            off += count * size
         # two snapshot slots per Receiver in a capturable loop body: the graph
         # copies the Receiver's data there; the transfer stream fetches it
         fetch_bytes = [0]
@@ -422,7 +443,7 @@ class HIPDevice(Device):
         if isinstance(cmd, Feeder):
             if self._capturing:
                 # inside a graph: copy this iteration's data from the staging slot
-                self.ctx.copy(self._feeder_dst(cmd), self._feeder_slots[cmd.id][self._parity], 4 * prod(cmd.shape))
+                self.ctx.copy(self._feeder_dst(cmd), self._feeder_slots[cmd.id][self._slot], 4 * prod(cmd.shape))
                 self._graph_feeders.append(cmd)
                 return
             arr = self._feeder_value(cmd)
@@ -502,32 +523,27 @@ class HIPDevice(Device):
             for _ in range(reps):
                 self._run_scheduled(inner)
             return
+        U = self._unroll.get(cmd.id, 1)
         if cmd.id not in self._graphs:
-            graphs = []
-            for parity in (0, 1):            # one graph per staging slot
-                self._capturing, self._parity = True, parity
-                self._graph_feeders = []
-                self._graph_receivers = []
-                self.ctx.graph_begin()
-                try:
-                    self._run_scheduled(inner)
-                finally:
-                    self._capturing = False
-                    graphs.append(self.ctx.graph_end())
-                if not self._graph_feeders and not self._graph_receivers:
-                    break                    # one graph serves every iteration
-            self._graphs[cmd.id] = (graphs, self._graph_feeders, self._graph_receivers)
-            self._iteration[cmd.id] = 0
-        graphs, feeders, receivers = self._graphs[cmd.id]
+            singles = self._capture(inner, U, 1)
+            feeders, receivers = self._graph_feeders, self._graph_receivers
+            unrolled = self._capture(inner, U, U) if U > 1 else None
+            self._graphs[cmd.id] = (singles, unrolled, feeders, receivers)
+            self._launches[cmd.id] = 0
+        singles, unrolled, feeders, receivers = self._graphs[cmd.id]
         waiting = []                         # fetched iterations whose callbacks are due
-        for _ in range(reps):
-            parity = self._iteration[cmd.id] & 1
+        done = 0
+        while done < reps:
+            n = U if unrolled is not None and reps - done >= U else 1
+            graphs = unrolled if n > 1 else singles
+            parity = self._launches[cmd.id] & 1
             if feeders:
-                # this iteration's inputs go up on the transfer stream while the
-                # previous iteration computes; the graph waits for them
+                # the inputs of these iterations go up on the transfer stream
+                # while the previous launch computes; the graph waits for them
                 self.ctx.stage_begin(parity)
-                for f in feeders:
-                    self.ctx.stage_write(parity, self._feeder_slots[f.id][parity], self._feeder_value(f))
+                for u in range(n):
+                    for f in feeders:
+                        self.ctx.stage_write(parity, self._feeder_slots[f.id][parity * U + u], self._feeder_value(f))
                 self.ctx.stage_end(parity)
             self.ctx.graph_launch(graphs[parity if len(graphs) > 1 else 0])
             if feeders:
@@ -540,9 +556,31 @@ class HIPDevice(Device):
                 waiting.append((parity, taken))
                 if len(waiting) > self.receiver_lag:
                     self._deliver(*waiting.pop(0))
-            self._iteration[cmd.id] += 1
+            self._launches[cmd.id] += 1
+            done += n
         for item in waiting:
             self._deliver(*item)
+
+    def _capture(self, inner, unroll, count):
+        """Graphs of ``count`` consecutive iterations of a loop body, one per
+        staging parity (one only when the body has no Feeder or Receiver);
+        iteration u of parity p reads Feeder slot ``p * unroll + u``."""
+        graphs = []
+        for parity in (0, 1):
+            self._capturing, self._parity = True, parity
+            self._graph_feeders = []
+            self._graph_receivers = []
+            self.ctx.graph_begin()
+            try:
+                for u in range(count):
+                    self._slot = parity * unroll + u
+                    self._run_scheduled(inner)
+            finally:
+                self._capturing = False
+                graphs.append(self.ctx.graph_end())
+            if not self._graph_feeders and not self._graph_receivers:
+                break                    # one graph serves every launch
+        return graphs
 
     def _fetch_receiver(self, r, parity):
         src = self._recv_slots[r.id][0][parity]
@@ -624,8 +662,8 @@ class HIPDevice(Device):
             content.reshape(-1)[:] = out
 
     def close(self):
-        for graphs, _, _ in self._graphs.values():
-            for g in graphs:
+        for singles, unrolled, _, _ in self._graphs.values():
+            for g in singles + (unrolled or []):
                 self.ctx.graph_destroy(g)
         self._graphs = {}
         self.ctx.close()

@@ -233,11 +233,13 @@ def test_column_reduce_split(hip, rows, cols):
     assert np.array_equal(got["m"], want["m"])
 
 
-@pytest.mark.parametrize("iters", [1, 2, 7, 50])
+@pytest.mark.parametrize("iters", [1, 2, 7, 50, 100])
 def test_feeder_values_reach_every_iteration(hip, iters):
     """A loop accumulates a value fed by the host each iteration (1, 2, ...):
     the staged copies on the transfer stream must land before, and only
-    before, the iteration that reads them.  The sum is exact in fp32."""
+    before, the iteration that reads them -- in graphs of one iteration and
+    in unrolled graphs of 32 (50 = 32 + 18 single launches, 100 = 3 x 32 + 4).
+    The sum is exact in fp32."""
     holder = [Tensor(np.zeros((4, 64), dtype=np.float32))]
     count = [0]
 
