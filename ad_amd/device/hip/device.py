@@ -15,17 +15,18 @@ replays loop bodies, ``execute`` runs both passes.  Differences by design:
   (``schedule``): launches ordered by their memory conflicts, independent
   launches of one kernel merged into one launch; the groups can be spread
   over several streams with event edges only where they touch overlapping
-  memory (``lanes``; one stream by default, see ``__init__``);
+  memory (``lanes``; one stream by default, see the class notes);
 * a loop body without nested loops is captured once as a HIP graph and the
-  graph is replayed ``len(r)`` times; a Feeder inside it copies from one of
-  two staging slots, which the host refills on a transfer stream while the
-  previous iteration computes (two graphs, one per slot); a Receiver inside
+  graph is replayed ``len(r)`` times (short bodies without Receivers also as
+  graphs of several iterations); a Feeder inside it copies from its staging
+  slot, which the host refills on a transfer stream while the previous
+  launch computes (two sets of slots and graphs); a Receiver inside
   it copies its data into one of two snapshot slots, which the transfer
   stream brings to pinned host memory after the iteration, and its
   callback runs before the next iteration is launched (``receiver_lag``
   0) or one iteration later (1);
 * a Feeder writes at its arena offset (the reference OpenCL backend writes
-  at offset 0, cl_helper.py:316,326 -- see ``oracle``);
+  at offset 0, cl_helper.py:316,326; ``feeder_offset_zero`` does that);
 * after the run, every Tensor's host array is refreshed from the device, as
   the reference's CL_MEM_USE_HOST_PTR buffers are on a CPU device.
 """
@@ -71,52 +72,58 @@ class _Launch:
 
 
 class HIPDevice(Device):
+    """The reference's device protocol on one MI355X (see the module notes).
+
+    Options (defaults give the reference's results):
+
+    * ``use_graphs`` -- replay loop bodies as HIP graphs (else launch by launch);
+    * ``group_launches`` -- run independent launches of one kernel as one
+      launch (argument rows selected by ``blockIdx.z``);
+    * ``lanes`` -- streams for independent launch groups in uncaptured runs.
+      Capture always uses one: capturing the C4 training step on four lanes
+      ended in a host segmentation fault inside
+      hipStreamEndCapture/hipGraphInstantiate whose cause is not established;
+    * ``loop_unroll`` -- a loop body without Receivers is also captured as a
+      graph of up to this many consecutive iterations (at most
+      ``UNROLL_LAUNCHES`` kernel commands per graph);
+    * ``receiver_lag`` -- a Receiver inside a replayed loop calls back before
+      the next iteration is launched (0, the reference's order) or one
+      iteration later (1: the next iteration computes meanwhile, and its
+      Feeders are called first);
+    * ``exact_reduce`` -- reductions combine all R elements (the reference's
+      work-group tree drops elements for non-power-of-two lengths and pads
+      MAX with 0, reduce.py:33-43);
+    * ``feeder_offset_zero`` -- a Feeder writes at offset 0 of its buffer, as
+      the OpenCL backend does (cl_helper.py:316,326); by default it honours
+      the arena offset, as the CUDA backend does (cuda_helper.py:117-119);
+    * ``strict_temps`` -- raise on a fused temp read through a non-identity
+      access, which the reference silently reads as the element's own value
+      (karg.py:47-48);
+    * ``dot_precision`` -- "bf16" (beyond the reference, which computes in
+      fp32): DotProd operands rounded to bfloat16, products summed in fp32 on
+      bf16 MFMA.
+    """
+
     def __init__(self, device_index: int = 0, use_graphs: bool = True, jit_threads: int = None,
                  group_launches: bool = True, lanes: int = 1, receiver_lag: int = 0,
                  exact_reduce: bool = False, feeder_offset_zero: bool = False,
                  strict_temps: bool = False, dot_precision: str = "fp32", loop_unroll: int = 32):
         super().__init__()
-        # fixes of reference behaviours, off by default (the reference's results):
-        # exact_reduce: reductions combine all R elements (the reference's
-        #   work-group tree drops elements for non-power-of-two lengths and
-        #   pads MAX with 0, reduce.py:33-43);
-        # feeder_offset_zero: a Feeder writes at offset 0 of its buffer, as the
-        #   OpenCL backend does (cl_helper.py:316,326) -- the default honours
-        #   the arena offset, as the CUDA backend does (cuda_helper.py:117-119);
-        # strict_temps: raise on a fused temp read through a non-identity
-        #   access, which the reference silently reads as the element's own
-        #   value (karg.py:47-48).
-        # dot_precision "bf16" (beyond the reference, which computes in fp32):
-        #   DotProd operands rounded to bfloat16, products summed in fp32 on
-        #   bf16 MFMA.
         assert dot_precision in ("fp32", "bf16"), "dot_precision must be fp32 or bf16"
-        self.exact_reduce = exact_reduce
-        # a replayed loop body without Receivers is also captured as a graph of
-        # up to `loop_unroll` consecutive iterations (bounded by UNROLL_LAUNCHES
-        # kernel commands per graph), so short bodies pay one graph launch and
-        # one staging round per several iterations
+        assert receiver_lag in (0, 1), "receiver_lag must be 0 or 1"
+        self.use_graphs = use_graphs
+        self.group_launches = group_launches
+        self.lanes = max(1, lanes)
         self.loop_unroll = max(1, loop_unroll)
-        self._plan_opts = codegen.PlanOptions(exact_reduce=exact_reduce, dot=dot_precision)
+        self.receiver_lag = receiver_lag
+        self.exact_reduce = exact_reduce
         self.feeder_offset_zero = feeder_offset_zero
         self.strict_temps = strict_temps
-        # Receivers inside a replayed loop: their callbacks run this many
-        # iterations after the iteration that produced the data (0: before
-        # the next iteration starts, the reference's order; 1: the next
-        # iteration computes meanwhile, and its Feeders are called first)
-        assert receiver_lag in (0, 1), "receiver_lag must be 0 or 1"
-        self.receiver_lag = receiver_lag
+        self._plan_opts = codegen.PlanOptions(exact_reduce=exact_reduce, dot=dot_precision)
         self.kernels = {}            # program_id -> [KernelPlan]
         self.funcs = {}              # program_id -> launch callable (ungrouped)
         self.buffers = {}            # buffer id -> arena byte offset
         self.buffers_size = {}       # buffer id -> floats
-        self.use_graphs = use_graphs
-        self.group_launches = group_launches
-        # parallel streams for independent launch groups in uncaptured runs
-        # (eager launches).  Graph capture always uses one lane: capturing
-        # the C4 training step on four lanes ended in a host segmentation
-        # fault inside hipStreamEndCapture/hipGraphInstantiate whose cause is
-        # not established.
-        self.lanes = max(1, lanes)
         self._events = 0             # event pool entries used by the schedules
         self.jit_threads = jit_threads or min(16, (os.cpu_count() or 4))
         self.ctx = Context(device_index)
