@@ -10,7 +10,7 @@ import ad_amd as ad
 from ad_amd import workloads
 from ad_amd.alloc import AllocEntry, DeallocEntry
 from ad_amd.device.hip import codegen
-from ad_amd.device.hip.schedule import RangeLevels, schedule
+from ad_amd.device.hip.schedule import RangeDeps, schedule_dag
 from ad_amd.graph import Feeder, ForNode, Receiver
 from oracle import OracleDevice
 
@@ -36,7 +36,7 @@ def test_schedule_keeps_conflicting_launches_in_order(seed):
                 out.append((rng.choice("ab"), lo, lo + rng.randint(0, 12)))
             return out
         launches.append((rng.choice("xyz"), rnd(), rnd()))
-    groups = schedule(launches, group_key=lambda item: item)
+    groups, _ = schedule_dag(launches, group_key=lambda item: item)
     order = [i for g in groups for i in g]
     assert sorted(order) == list(range(len(launches)))
     pos = {i: k for k, i in enumerate(order)}
@@ -50,15 +50,15 @@ def test_schedule_keeps_conflicting_launches_in_order(seed):
         assert len({launches[i][0] for i in g}) == 1
 
 
-def test_range_levels_split_segments():
-    t = RangeLevels()
-    assert t.level_for([], [("a", 0, 10)]) == 0
-    t.record([], [("a", 0, 10)], 0)
-    assert t.level_for([("a", 10, 20)], []) == 0      # touching, not overlapping
-    assert t.level_for([("a", 9, 20)], []) == 1
-    t.record([("a", 5, 7)], [], 3)
-    assert t.level_for([], [("a", 6, 8)]) == 4          # write after the read
-    assert t.level_for([], [("a", 7, 9)]) == 1
+def test_range_deps_split_segments():
+    t = RangeDeps()
+    assert t.access(0, [], [("a", 0, 10)]) == set()
+    assert t.access(1, [("a", 10, 20)], []) == set()     # touching, not overlapping
+    assert t.access(2, [("a", 9, 20)], []) == {0}
+    assert t.access(3, [("a", 5, 7)], []) == {0}
+    assert t.access(4, [], [("a", 6, 8)]) == {0, 3}      # after the writer and the readers since
+    assert t.access(5, [], [("a", 7, 9)]) == {0, 4}
+    assert t.access(6, [("b", 0, 100)], [("a", 0, 1)]) == {0}
 
 
 def _regions(proc):
@@ -84,7 +84,7 @@ def _reorder(proc, info):
         for cmd in stretch:
             reads, writes = codegen.command_regions(cmd, info)
             launches.append((cmd, reads, writes))
-        for g in schedule(launches, group_key=lambda c: None):
+        for g in schedule_dag(launches, group_key=lambda c: None)[0]:
             out.extend(launches[i][0] for i in g)
         stretch.clear()
 
