@@ -10,12 +10,16 @@ statements ``kres = f(kargs)`` evaluated per element; temps are registers;
 constants are double literals (``str(float)``), so ``x * c`` is computed in
 double and rounded to float, exactly as the OpenCL source does.
 
-Where the reference relies on all work-items of a work-group running in
-lockstep -- a statement writing a region that another element of the same
-kernel still reads, which the tetris allocator produces when a value dies
-inside a fused group -- the command is emitted as a sequence of kernels,
-one per statement, each staging its result before storing it
-(``lockstep`` plans).  ``hazards`` decides which commands need that.
+Where a statement writes a location another element of the same command
+still reads (the tetris allocator places a value born inside a fused group
+over one that dies there), the reference's single kernel races; the result
+kept here is the statement-by-statement one.  ``conflict_pairs`` finds those
+statement pairs, ``split_phases`` cuts the command into the fewest passes
+with no conflict inside a pass (temps carried through scratch), and a
+statement that conflicts with itself falls back to one staged kernel per
+statement (``lockstep_plans``).  A DotProd or Reduce runs in the first pass
+that needs it, with the epilogue in registers or, split over K / rows, as
+partial results combined by an elementwise pass (``first_pass_plans``).
 """
 import hashlib
 import math
@@ -337,11 +341,6 @@ def components(stmts, buffers: BufferInfo):
     for i in range(len(stmts)):
         groups.setdefault(find(i), []).append(stmts[i])
     return [groups[r] for r in sorted(groups)]
-
-
-def hazards(stmts, buffers: BufferInfo, index_kind: str, n_cols: int = 1) -> bool:
-    """True when the command needs more than one pass over its elements."""
-    return len(conflict_pairs(stmts, buffers, index_kind, n_cols)) > 0
 
 
 # ------------------------------------------------------------------ lowering helpers
