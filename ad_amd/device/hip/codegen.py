@@ -409,10 +409,12 @@ _NO_SIZES = BufferInfo()
 class PlanOptions:
     """Choices that change results, all off by default (the reference's):
     ``exact_reduce`` -- reductions combine every element (``kept_elements``);
-    ``dot`` -- "bf16" rounds DotProd operands to bfloat16 and sums in fp32 on
-    bf16 MFMA (``pack_plan``, ``dotprod_bf16_plan``)."""
+    ``dot`` -- "bf16" rounds the operands of DotProds of at least
+    ``bf16_min_macs`` multiply-adds to bfloat16 and sums in fp32 on bf16 MFMA
+    (``pack_plan``, ``dotprod_bf16_plan``); smaller ones stay fp32."""
     exact_reduce: bool = False
     dot: str = "fp32"
+    bf16_min_macs: int = 1 << 30
 
 
 DEFAULT_OPTIONS = PlanOptions()
@@ -1435,7 +1437,7 @@ def first_pass_plans(part, n, init_node, alloc: ScratchAlloc, opts=DEFAULT_OPTIO
         K = init_node.children_shapes[0][1]
         cfg = dp_config(M, N, K)
         A, B = init_node.kargs
-        if opts.dot == "bf16":
+        if opts.dot == "bf16" and M * N * K >= opts.bf16_min_macs:
             # both operands packed to k-contiguous bf16 in scratch, then the product
             m_pad, n_pad, k_pad = bf16_dims(M, N, K, cfg)
             a_off = alloc.take((m_pad * k_pad + 1) // 2)

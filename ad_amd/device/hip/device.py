@@ -100,14 +100,17 @@ class HIPDevice(Device):
       access, which the reference silently reads as the element's own value
       (karg.py:47-48);
     * ``dot_precision`` -- "bf16" (beyond the reference, which computes in
-      fp32): DotProd operands rounded to bfloat16, products summed in fp32 on
+      fp32): the operands of DotProds of at least ``bf16_min_macs``
+      multiply-adds (2^30 by default: smaller products gain less than their
+      operand packing costs) rounded to bfloat16, products summed in fp32 on
       bf16 MFMA.
     """
 
     def __init__(self, device_index: int = 0, use_graphs: bool = True, jit_threads: int = None,
                  group_launches: bool = True, lanes: int = 1, receiver_lag: int = 0,
                  exact_reduce: bool = False, feeder_offset_zero: bool = False,
-                 strict_temps: bool = False, dot_precision: str = "fp32", loop_unroll: int = 32):
+                 strict_temps: bool = False, dot_precision: str = "fp32", bf16_min_macs: int = 1 << 30,
+                 loop_unroll: int = 32):
         super().__init__()
         assert dot_precision in ("fp32", "bf16"), "dot_precision must be fp32 or bf16"
         assert receiver_lag in (0, 1), "receiver_lag must be 0 or 1"
@@ -119,7 +122,8 @@ class HIPDevice(Device):
         self.exact_reduce = exact_reduce
         self.feeder_offset_zero = feeder_offset_zero
         self.strict_temps = strict_temps
-        self._plan_opts = codegen.PlanOptions(exact_reduce=exact_reduce, dot=dot_precision)
+        self._plan_opts = codegen.PlanOptions(exact_reduce=exact_reduce, dot=dot_precision,
+                                              bf16_min_macs=bf16_min_macs)
         self.kernels = {}            # program_id -> [KernelPlan]
         self.funcs = {}              # program_id -> launch callable (ungrouped)
         self.buffers = {}            # buffer id -> arena byte offset

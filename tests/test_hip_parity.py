@@ -380,7 +380,7 @@ def test_bf16_dotprod_bound(hip, M, K, N, ta, tb):
     r = ((Tensor(a).T() if ta else Tensor(a)) @ (Tensor(b).T() if tb else Tensor(b))) + Tensor(bias)
     got = {}
     Receiver(lambda v: got.setdefault("r", v.copy()), [r])
-    ad.execute(device=hip(dot_precision="bf16"))
+    ad.execute(device=hip(dot_precision="bf16", bf16_min_macs=0))
     aa = (a.T if ta else a).astype(np.float64)
     bb = (b.T if tb else b).astype(np.float64)
     ref = aa @ bb + bias
@@ -398,7 +398,23 @@ def test_bf16_training_steps(hip):
     by about 1 %)."""
     from ad_amd import workloads
     a, b = run_both(lambda: workloads.transformer(layers=1, d_model=64, heads=4, ff=128, seq=16, batch=2,
-                                                  steps=3), lambda: hip(dot_precision="bf16"))
+                                                  steps=3), lambda: hip(dot_precision="bf16", bf16_min_macs=0))
     for x, y in zip(a["params"], b["params"]):
         assert np.all(np.isfinite(x))
         np.testing.assert_allclose(x, y, rtol=0, atol=2e-3)
+
+
+def test_bf16_leaves_small_products_fp32(hip):
+    """Under dot_precision="bf16", DotProds below bf16_min_macs run the fp32
+    kernel: the result equals the fp32 backend's bit for bit."""
+    rng = np.random.default_rng(5)
+    a = rng.standard_normal((256, 256)).astype(np.float32)
+    b = rng.standard_normal((256, 256)).astype(np.float32)
+    out = []
+    for dev in (hip(dot_precision="bf16"), hip()):
+        ad.reset()
+        got = {}
+        Receiver(lambda v: got.setdefault("r", v.copy()), [Tensor(a) @ Tensor(b)])
+        ad.execute(device=dev)
+        out.append(got["r"])
+    assert np.array_equal(out[0], out[1])
