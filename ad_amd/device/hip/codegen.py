@@ -60,7 +60,7 @@ class KernelPlan:
     source: str                   # full source; the kernel symbol is ``name``
     grid: Tuple[int, int, int]
     block: Tuple[int, int, int]
-    args: List[tuple]             # ("buf", buffer_id, float_offset) | ("scratch", float_offset) | ("int", v)
+    args: List[tuple]             # ("buf", buffer_id, float_offset) | ("var", (buffer_id, var_id, var_offset, size), float_offset) | ("scratch", float_offset) | ("int", v)
     shared: int = 0
     family: str = ""              # "elw" | "reduce" | "dotprod" | "copy"
     flops: int = 0                # algorithmic flops (dotprod) for reporting
@@ -145,20 +145,38 @@ def _iter_kmatrix(karg):
         yield from _iter_kmatrix(karg.karg_two)
 
 
+iter_kmatrix = _iter_kmatrix
+
+
 # ------------------------------------------------------------------ hazards
 class BufferInfo:
-    """Per buffer id: total floats, and per tetris variable region."""
+    """Per buffer id: total floats.  ``unpacked``: every tetris variable has
+    storage of its own (no two variables share memory), instead of its
+    packed offset in the tetris region."""
 
-    def __init__(self):
+    def __init__(self, unpacked: bool = False):
         self.size: Dict[int, int] = {}
+        self.unpacked = unpacked
 
 
 def _region(km: KMatrix, buffers: BufferInfo):
     var = getattr(km, "tetris_var", None)
     if var is not None:
-        _, off, size = var
-        return (km.id, off, off + size), var[0]
+        vid, off, size = var
+        if buffers.unpacked:
+            return (("tv", vid), 0, size), vid
+        return (km.id, off, off + size), vid
     return (km.id, 0, buffers.size.get(km.id, 1 << 62)), ("buf", km.id)
+
+
+def _km_ptr(params, km: KMatrix, c: int) -> str:
+    """The pointer parameter of a buffer access with folded offset ``c``: a
+    tetris variable is addressed relative to its own start (its storage is
+    placed by the device), any other buffer relative to the buffer."""
+    var = getattr(km, "tetris_var", None)
+    if var is not None:
+        return params.ptr("var", (km.id,) + tuple(var), c - var[1])
+    return params.ptr("buf", km.id, c)
 
 
 def _unval(e):
@@ -506,7 +524,7 @@ class Lowerer:
         if getattr(km, "scratch_offset", None) is not None:
             p = self.params.ptr("scratch", 0, km.scratch_offset + c)
         else:
-            p = self.params.ptr("buf", km.id, c)
+            p = _km_ptr(self.params, km, c)
         idx = lower_index(core, self.ity)
         return p, idx, (p, repr(core))
 
@@ -624,7 +642,7 @@ def _params_decl(params: Params) -> str:
 def _plan_args(params: Params, extra_ints=()) -> List[tuple]:
     out = []
     for kind, ident, off in params.slots:
-        out.append(("scratch", off) if kind == "scratch" else ("buf", ident, off))
+        out.append(("scratch", off) if kind == "scratch" else (kind, ident, off))
     out.extend(("int", v) for v in extra_ints)
     return out
 
@@ -753,7 +771,7 @@ def _vector_lines(stmts, ity, params: Params, index_kind="global", hoist=None) -
         if getattr(km, "scratch_offset", None) is not None:
             p = params.ptr("scratch", 0, km.scratch_offset + c)
         else:
-            p = params.ptr("buf", km.id, c)
+            p = _km_ptr(params, km, c)
         return p, core, (p, repr(core))
 
     def vec_expr(k):
@@ -905,7 +923,7 @@ def _loader_struct(name, karg, role, params: Params, ity, dims) -> Tuple[str, bo
     if getattr(karg, "scratch_offset", None) is not None:
         p = params.ptr("scratch", 0, karg.scratch_offset + c)
     else:
-        p = params.ptr("buf", karg.id, c)
+        p = _km_ptr(params, karg, c)
     idx = lower_index(core, ity)
     # A: mode 0 contiguous along k (= _y); B: mode 0 contiguous along n (= _y)
     vy = vec_class(core, Y)
@@ -1189,7 +1207,7 @@ def reduce_plan(stmts, red, partial_off=None, exact=False) -> KernelPlan:
             at4 = "return make_float4(0.f, 0.f, 0.f, 0.f);"
         else:
             core, c = split_const(karg.access)
-            p = params.ptr("buf", karg.id, c)
+            p = _km_ptr(params, karg, c)
             idx = lower_index(core, ity)
             at = f"return {p}[{idx}];"
             at4 = f"return *reinterpret_cast<const float4*>({p} + {idx});"

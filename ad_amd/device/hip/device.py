@@ -103,15 +103,25 @@ class HIPDevice(Device):
       fp32): the operands of DotProds of at least ``bf16_min_macs``
       multiply-adds (2^30 by default: smaller products gain less than their
       operand packing costs) rounded to bfloat16, products summed in fp32 on
-      bf16 MFMA.
+      bf16 MFMA;
+    * ``arena`` -- "packed" (the reference's layout: every tetris variable
+      at its packed offset, variables with disjoint lifetimes sharing
+      memory) or "unpacked" (beyond the reference: every tetris variable in
+      storage of its own, so reuse of memory between variables orders no
+      launches; costs the sum of the variables' sizes instead of the packed
+      high-water mark).
     """
 
     def __init__(self, device_index: int = 0, use_graphs: bool = True, jit_threads: int = None,
                  group_launches: bool = True, lanes: int = 1, receiver_lag: int = 0,
                  exact_reduce: bool = False, feeder_offset_zero: bool = False,
                  strict_temps: bool = False, dot_precision: str = "fp32", bf16_min_macs: int = 1 << 30,
-                 loop_unroll: int = 32):
+                 loop_unroll: int = 32, arena: str = "packed"):
         super().__init__()
+        assert arena in ("packed", "unpacked"), "arena must be packed or unpacked"
+        assert not (arena == "unpacked" and feeder_offset_zero), \
+            "feeder_offset_zero writes into the packed arena; it needs arena='packed'"
+        self.arena = arena
         assert dot_precision in ("fp32", "bf16"), "dot_precision must be fp32 or bf16"
         assert receiver_lag in (0, 1), "receiver_lag must be 0 or 1"
         self.use_graphs = use_graphs
@@ -128,6 +138,8 @@ class HIPDevice(Device):
         self.funcs = {}              # program_id -> launch callable (ungrouped)
         self.buffers = {}            # buffer id -> arena byte offset
         self.buffers_size = {}       # buffer id -> floats
+        self._vars = {}              # tetris variable id -> (packed float offset, floats)
+        self._var_off = {}           # tetris variable id -> arena byte offset (unpacked arena)
         self._events = 0             # event pool entries used by the schedules
         self.jit_threads = jit_threads or min(16, (os.cpu_count() or 4))
         self.ctx = Context(device_index)
@@ -151,12 +163,15 @@ class HIPDevice(Device):
     def init(self, cmd):
         if isinstance(cmd, Feeder):
             cmd.kres.calc_offset()
+            self._note_vars(cmd.kres)
             self._feeder_slots[cmd.id] = None
             return
         if isinstance(cmd, Receiver):
-            cmd.offsets, cmd.shapes, cmd.ids = [], [], []
+            cmd.offsets, cmd.shapes, cmd.ids, cmd.vars = [], [], [], []
             for k in cmd.kargs:
                 k.calc_offset()
+                self._note_vars(k)
+                cmd.vars.append(getattr(k, "tetris_var", None))
                 cmd.ids.append(k.id)
                 cmd.shapes.append(k.shape)
                 cmd.offsets.append(k.offset)
@@ -168,14 +183,27 @@ class HIPDevice(Device):
         if isinstance(cmd, (DeallocEntry, ForNode)):
             return
         if isinstance(cmd, (Node, FuseBase)):
+            for n in (cmd.nodes if isinstance(cmd, FuseBase) else [cmd]):
+                if not isinstance(n, Node):
+                    continue
+                for k in n.kargs:
+                    self._note_vars(k)
+                self._note_vars(n.kres)
             self._pending.append(cmd)
             return
         raise AssertionError(f"Encountered unexpected cmd: {cmd}")
 
+    def _note_vars(self, karg):
+        for km in codegen.iter_kmatrix(karg):
+            var = getattr(km, "tetris_var", None)
+            if var is not None:
+                self._vars[var[0]] = (var[1], var[2])
+
     def _layout(self):
-        """Byte offset of every non-temp buffer, in AllocEntry order."""
+        """Byte offset of every non-temp buffer, in AllocEntry order; with the
+        unpacked arena, then one region per tetris variable, by variable id."""
         off = 0
-        info = codegen.BufferInfo()
+        info = codegen.BufferInfo(unpacked=self.arena == "unpacked")
         for a in self._allocs:
             self.buffers[a.id] = off
             self.buffers_size[a.id] = a.size
@@ -183,7 +211,22 @@ class HIPDevice(Device):
             if a.content is not None:
                 self._contents[a.id] = a.content
             off += _align(a.size * 4)
+        if info.unpacked:
+            # each variable starts at the same address modulo ALIGN as at its
+            # packed offset, so every alignment a kernel was planned for holds
+            for vid in sorted(self._vars):
+                voff, size = self._vars[vid]
+                self._var_off[vid] = off + 4 * voff % ALIGN
+                off = _align(self._var_off[vid] + 4 * size)
         return off, info
+
+    def _addr(self, bid, off, var):
+        """Arena byte offset of float ``off`` of buffer ``bid``; ``var`` is the
+        tetris variable (id, packed offset, size) the access belongs to, or
+        None."""
+        if var is not None and self._var_off:
+            return self._var_off[var[0]] + 4 * (off - var[1])
+        return self.buffers[bid] + 4 * off
 
     def _finish_init(self, proc):
         off, info = self._layout()
@@ -325,7 +368,9 @@ class HIPDevice(Device):
                              f"{tid} through the access {acc}; the reference reads that element's own value")
 
     def _feeder_dst(self, cmd):
-        return self.buffers[cmd.kres.id] + (0 if self.feeder_offset_zero else 4 * cmd.kres.offset)
+        if self.feeder_offset_zero:
+            return self.buffers[cmd.kres.id]
+        return self._addr(cmd.kres.id, cmd.kres.offset, getattr(cmd.kres, "tetris_var", None))
 
     def _arg_values(self, plan, pid):
         """Argument row of a plan of command ``pid``: ``(True, arena byte
@@ -335,6 +380,9 @@ class HIPDevice(Device):
         for a in plan.args:
             if a[0] == "buf":
                 vals.append((True, self.buffers[a[1]] + 4 * a[2]))
+            elif a[0] == "var":
+                bid, vid, voff, size = a[1]
+                vals.append((True, self._addr(bid, voff + a[2], (vid, voff, size))))
             elif a[0] == "scratch":
                 vals.append((True, self.scratch_off + 4 * (self._scratch_base[pid] + a[1])))
             else:
@@ -464,16 +512,16 @@ class HIPDevice(Device):
             if self._capturing:
                 # inside a graph: snapshot the data into this iteration's slot
                 dst = self._recv_slots[cmd.id][0][self._parity]
-                for bid, shape, off in zip(cmd.ids, cmd.shapes, cmd.offsets):
+                for bid, shape, off, var in zip(cmd.ids, cmd.shapes, cmd.offsets, cmd.vars):
                     n = 4 * prod(shape)
-                    self.ctx.copy(dst, self.buffers[bid] + 4 * off, n)
+                    self.ctx.copy(dst, self._addr(bid, off, var), n)
                     dst += _align(n)
                 self._graph_receivers.append(cmd)
                 return
             outs = []
-            for bid, shape, off in zip(cmd.ids, cmd.shapes, cmd.offsets):
+            for bid, shape, off, var in zip(cmd.ids, cmd.shapes, cmd.offsets, cmd.vars):
                 out = np.empty(shape, dtype=np.float32)
-                self.ctx.read(self.buffers[bid] + 4 * off, out)
+                self.ctx.read(self._addr(bid, off, var), out)
                 outs.append(out)
             cmd.func(*outs)
             return

@@ -154,7 +154,7 @@ def micro_elw(reps, copies=2):
     return {"kernel": name, "ms": ms, "bytes": nbytes, "gbs": nbytes / ms / 1e6}
 
 
-def transformer_steps(config, steps, warmup, eager=False, lanes=1, dot="fp32"):
+def transformer_steps(config, steps, warmup, eager=False, lanes=1, dot="fp32", arena="packed"):
     import ad_amd as ad
     from ad_amd import workloads
     from ad_amd.device.hip import HIPDevice
@@ -167,7 +167,7 @@ def transformer_steps(config, steps, warmup, eager=False, lanes=1, dot="fp32"):
     t1 = time.perf_counter()
     step_flops = workloads.dotprod_flops(proc)
     log(f"{config}: traced + compiled in {t1 - t0:.1f} s; {step_flops / 1e12:.3f} TFLOP of DotProd per step")
-    dev = HIPDevice(use_graphs=not eager, lanes=lanes, dot_precision=dot)
+    dev = HIPDevice(use_graphs=not eager, lanes=lanes, dot_precision=dot, arena=arena)
     dev.prepare(proc)
     t2 = time.perf_counter()
     log(f"{config}: device init + JIT in {t2 - t1:.1f} s; {dev.stats}")
@@ -266,6 +266,15 @@ def other_configs():
         "dotprod_elw_4096_frac_of_bf16_peak": round(dp["tflops"] / PEAK_BF16_MFMA_TFLOPS, 4),
         "c5_steps_per_s": round(1e3 / ms, 2), "c5_ms_per_step": round(ms, 3)}
     log(f"bf16 DotProds: 4096^3 {dp['tflops']:.1f} TFLOP/s (packing included); c5 {1e3 / ms:.1f} steps/s")
+    unpacked = {"note": "option beyond the reference: every tetris variable in storage of its own, "
+                        "launches ordered by data flow only; fp32"}
+    for config in ("c4", "c5"):
+        r = transformer_steps(config, 20, 3, arena="unpacked")
+        ms = r["event_ms"] / 20
+        unpacked[f"{config}_steps_per_s"] = round(1e3 / ms, 2)
+        unpacked[f"{config}_launches_per_step"] = r["launches_per_step"]
+        log(f"unpacked arena: {config} {1e3 / ms:.1f} steps/s, {r['launches_per_step']} launches/step")
+    out["unpacked_arena"] = unpacked
     return out
 
 
@@ -327,6 +336,9 @@ def main():
                     help="streams for independent launch groups in eager runs (graphs use one)")
     ap.add_argument("--micro-only", action="store_true",
                     help="run only the single-command benchmarks (for counter passes)")
+    ap.add_argument("--arena", choices=["packed", "unpacked"], default="packed",
+                    help="packed: tetris variables at the reference's packed offsets (default); "
+                         "unpacked: each in storage of its own")
     ap.add_argument("--eager", action="store_true",
                     help="launch the step's kernels one by one instead of replaying a HIP graph "
                          "(for kernel-trace profilers)")
@@ -359,7 +371,8 @@ def main():
     if args.micro_only:
         print(json.dumps({"microbench": micro or None}), flush=True)
         return
-    tr = transformer_steps(args.config, args.steps, args.warmup, eager=args.eager, lanes=args.lanes)
+    tr = transformer_steps(args.config, args.steps, args.warmup, eager=args.eager, lanes=args.lanes,
+                           arena=args.arena)
     value = args.steps / tr["wall_s"]
     ms_per_step = tr["wall_s"] * 1e3 / args.steps
     log(f"{args.config}: {ms_per_step:.2f} ms/step wall, {tr['event_ms'] / args.steps:.2f} ms/step "
@@ -389,7 +402,8 @@ def main():
         "data": "synthetic",
         "config": {"workload": f"{args.config}: {layers}-layer transformer encoder fwd+bwd+SGD, "
                                f"d_model {d}, {h} heads, FFN {f} ReLU, seq {s}, batch {b}, fp32, "
-                               + ("eager launches" if args.eager else "one HIP-graph replay per step"),
+                               + ("eager launches" if args.eager else "one HIP-graph replay per step")
+                               + (", unpacked arena" if args.arena == "unpacked" else ""),
                    "layers": layers, "d_model": d, "heads": h, "ffn": f, "seq_len": s, "batch": b,
                    "parallelism": "none (1 GPU)"},
         "step_dotprod_tflops": round(tr["step_flops"] / (ms_per_step * 1e9), 2),
