@@ -18,8 +18,32 @@
 #pragma clang fp contract(off)
 
 typedef float adhip_f32x16 __attribute__((ext_vector_type(16)));
+typedef float adhip_f32x4 __attribute__((ext_vector_type(4)));
 
 namespace adhip {
+
+// float4 load / store of generated code; S = true streams the data
+// (nontemporal: the lines are not kept in the caches), for operands too
+// large for the caches to hold until anyone reads them again.
+template <bool S>
+__device__ __forceinline__ float4 ld4(const float* p) {
+  if constexpr (S) {
+    const adhip_f32x4 t = __builtin_nontemporal_load(reinterpret_cast<const adhip_f32x4*>(p));
+    return make_float4(t.x, t.y, t.z, t.w);
+  } else {
+    return *reinterpret_cast<const float4*>(p);
+  }
+}
+
+template <bool S>
+__device__ __forceinline__ void st4(float* p, float4 v) {
+  if constexpr (S) {
+    const adhip_f32x4 t = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(t, reinterpret_cast<adhip_f32x4*>(p));
+  } else {
+    *reinterpret_cast<float4*>(p) = v;
+  }
+}
 
 template <int OP>
 __device__ __forceinline__ float rop(float a, float b) {

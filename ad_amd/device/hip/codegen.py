@@ -420,6 +420,13 @@ def _scratch_km(off, access=None):
 
 
 HOIST_MAX = 8
+
+
+def _stream_arg(km) -> str:
+    """Template argument of ``adhip::ld4`` / ``st4`` for an access: true for
+    a KMatrix the device marked ``stream`` (data no other command reads)."""
+    return "true" if getattr(km, "stream", False) else "false"
+
 _NO_SIZES = BufferInfo()
 
 
@@ -790,7 +797,7 @@ def _vector_lines(stmts, ity, params: Params, index_kind="global", hoist=None) -
         idx = lower_index(core, ity)
         moving, zero = _moving(index_kind)
         if vec_class(core, moving, zero).kind == AFF:
-            return f"(*reinterpret_cast<const float4*>({p} + {idx}))"
+            return f"adhip::ld4<{_stream_arg(k)}>({p} + {idx})"
         v = f"{p}[{idx}]"
         return f"make_float4({v}, {v}, {v}, {v})"
 
@@ -895,7 +902,7 @@ def _vector_lines(stmts, ity, params: Params, index_kind="global", hoist=None) -
         p, core, key = loc(n.kres)
         r = fresh("w")
         lines.append(f"float4 {r}; {r}.x = {vals[0]}; {r}.y = {vals[1]}; {r}.z = {vals[2]}; {r}.w = {vals[3]};")
-        lines.append(f"*reinterpret_cast<float4*>({p} + {lower_index(core, ity)}) = {r};")
+        lines.append(f"adhip::st4<{_stream_arg(n.kres)}>({p} + {lower_index(core, ity)}, {r});")
         written[key] = r
         loaded.pop(key, None)
         if hoist is not None:
@@ -1210,7 +1217,7 @@ def reduce_plan(stmts, red, partial_off=None, exact=False) -> KernelPlan:
             p = _km_ptr(params, karg, c)
             idx = lower_index(core, ity)
             at = f"return {p}[{idx}];"
-            at4 = f"return *reinterpret_cast<const float4*>({p} + {idx});"
+            at4 = f"return adhip::ld4<{_stream_arg(karg)}>({p} + {idx});"
             vy = vec_class(core, Y)
             if vy.kind == AFF:
                 vec = vy.al and c % 4 == 0 and R % 4 == 0 and not dropped

@@ -109,19 +109,25 @@ class HIPDevice(Device):
       memory) or "unpacked" (beyond the reference: every tetris variable in
       storage of its own, so reuse of memory between variables orders no
       launches; costs the sum of the variables' sizes instead of the packed
-      high-water mark).
+      high-water mark);
+    * ``stream_min_bytes`` -- float4 reads of a range of at least this many
+      bytes that no other command reads (and no loop iteration reads again),
+      and writes of such a range no command reads, bypass the caches
+      (nontemporal), so they do not evict data that is read again (None:
+      never).  Results are unchanged.
     """
 
     def __init__(self, device_index: int = 0, use_graphs: bool = True, jit_threads: int = None,
                  group_launches: bool = True, lanes: int = 1, receiver_lag: int = 0,
                  exact_reduce: bool = False, feeder_offset_zero: bool = False,
                  strict_temps: bool = False, dot_precision: str = "fp32", bf16_min_macs: int = 1 << 30,
-                 loop_unroll: int = 32, arena: str = "packed"):
+                 loop_unroll: int = 32, arena: str = "packed", stream_min_bytes: int = 32 << 20):
         super().__init__()
         assert arena in ("packed", "unpacked"), "arena must be packed or unpacked"
         assert not (arena == "unpacked" and feeder_offset_zero), \
             "feeder_offset_zero writes into the packed arena; it needs arena='packed'"
         self.arena = arena
+        self.stream_min_bytes = stream_min_bytes
         assert dot_precision in ("fp32", "bf16"), "dot_precision must be fp32 or bf16"
         assert receiver_lag in (0, 1), "receiver_lag must be 0 or 1"
         self.use_graphs = use_graphs
@@ -220,6 +226,57 @@ class HIPDevice(Device):
                 off = _align(self._var_off[vid] + 4 * size)
         return off, info
 
+    def _mark_streams(self, proc, info):
+        """Mark the float4 accesses that bypass the caches (``km.stream``):
+        a read of a range (arena variable or buffer) that no other command
+        reads and, inside a loop body, that the body itself writes (a range
+        the body only reads is read again by the next iteration); a write of
+        a range no command reads.  Only ranges of at least
+        ``stream_min_bytes``: the caches keep smaller ones to good effect."""
+        readers, reads, writes = {}, [], []
+
+        def nodes(cmd):
+            return [n for n in (cmd.nodes if isinstance(cmd, FuseBase) else [cmd]) if isinstance(n, Node)]
+
+        def body_writes(body):
+            out = set()
+            for c in body.procedure:
+                if isinstance(c, ForNode):
+                    out |= body_writes(c.get_proc())
+                elif isinstance(c, (Node, FuseBase)) and not isinstance(c, Receiver):
+                    for n in ([c] if isinstance(c, Feeder) else nodes(c)):
+                        if not n.kres.is_none() and not n.kres.is_temp:
+                            out.add(codegen._region(n.kres, info)[0])
+            return out
+
+        def scan(body, own):
+            for c in body.procedure:
+                if isinstance(c, ForNode):
+                    scan(c.get_proc(), body_writes(c.get_proc()))
+                    continue
+                if isinstance(c, (Feeder, Receiver)) or not isinstance(c, (Node, FuseBase)):
+                    continue
+                for n in nodes(c):
+                    for k in n.kargs:
+                        for km in codegen.iter_kmatrix(k):
+                            if km.is_temp or getattr(km, "scratch_offset", None) is not None:
+                                continue
+                            r = codegen._region(km, info)[0]
+                            readers.setdefault(r, set()).add(c.program_id)
+                            if own is not None and r not in own:
+                                readers[r].add(None)        # read again every iteration
+                            reads.append((km, r))
+                    if not n.kres.is_none() and not n.kres.is_temp:
+                        writes.append((n.kres, codegen._region(n.kres, info)[0]))
+        scan(proc, None)
+        big = self.stream_min_bytes
+        for km, r in reads:
+            if len(readers[r]) == 1 and 4 * (r[2] - r[1]) >= big:
+                km.stream = True
+        for km, r in writes:
+            if r not in readers and 4 * (r[2] - r[1]) >= big:
+                km.stream = True
+
     def _addr(self, bid, off, var):
         """Arena byte offset of float ``off`` of buffer ``bid``; ``var`` is the
         tetris variable (id, packed offset, size) the access belongs to, or
@@ -266,6 +323,8 @@ class HIPDevice(Device):
         # kernel plans and the ranges each command touches; commands that need
         # scratch get consecutive slots of a ring, so neighbouring commands do
         # not share scratch and can run in one launch
+        if self.stream_min_bytes is not None:
+            self._mark_streams(proc, info)
         plans, regions, needs = {}, {}, {}
         for cmd in self._pending:
             if self.strict_temps:
