@@ -93,6 +93,9 @@ class KernelPlan:
 _ENTRY_RE = re.compile(r'extern "C" __global__ void __launch_bounds__\((\d+)\) ' + "adhip_kernel" + r"\(([^)]*)\) \{")
 
 
+LAZY_ARGS = 24
+
+
 def _table_entry(src: str, nargs: int) -> str:
     """Turn the generated kernel (the last function of ``src``) into a device
     function plus an entry point whose only parameter is an argument table
@@ -109,7 +112,25 @@ def _table_entry(src: str, nargs: int) -> str:
     casts = []
     for i, q in enumerate(plist):
         ty = q.rsplit(" ", 1)[0]
-        casts.append(f"({ty})a_[{i}]")
+        if ty.endswith("*"):
+            # a pointer read from memory is generic (flat loads, which also
+            # count against the LDS wait counter); it points to global
+            # memory, and saying so gives global loads and stores
+            casts.append(f"({ty})({ty[:-1].strip()} __attribute__((address_space(1)))*)a_[{i}]")
+        else:
+            casts.append(f"({ty})a_[{i}]")
+    if nargs > LAZY_ARGS:
+        # many arguments (a concat of many pieces): read each one from the
+        # table where it is used, so a wave loads only the pieces its
+        # elements take instead of holding (and spilling) all of them
+        for i, q in enumerate(plist):
+            name = q.rsplit(" ", 1)[1]
+            body = re.sub(rf"\b{re.escape(name)}\b", f"({casts[i]})", body)
+        return (src[:m.start()] +
+                f'extern "C" __global__ void __launch_bounds__({bounds}) {KNAME}('
+                f"const unsigned long long* __restrict__ tbl_) {{\n"
+                f"  const unsigned long long* a_ = tbl_ + (unsigned long long)blockIdx.z * {nargs}u;\n"
+                f"{body}}}\n")
     return (src[:m.start()] +
             f"static __device__ __forceinline__ void {KNAME}_body({params}) {{{body}}}\n"
             f'extern "C" __global__ void __launch_bounds__({bounds}) {KNAME}('
@@ -717,6 +738,9 @@ def _index_setup(index_kind, ity, n_cols):
     return ""
 
 
+SCALAR_MAX_N, SCALAR_MIN_STMTS = 1 << 18, 8
+
+
 def elementwise_plan(stmts, n, index_kind="global", n_cols=1, flops=0, init_value=None) -> KernelPlan:
     """One thread per element (or per 4 elements when every access allows a
     float4), statements in order.  ``index_kind`` defines ``_x``/``_y`` for
@@ -726,7 +750,12 @@ def elementwise_plan(stmts, n, index_kind="global", n_cols=1, flops=0, init_valu
     bound = _expr_bound(stmts, max(n - 1, 0), max(n - 1, 0), max(n_cols - 1, 0))
     ity = _ity(bound)
     setup = _index_setup(index_kind, ity, n_cols)
-    if not _vector_plan(stmts, n, index_kind, n_cols):
+    # a short pass with long statement chains runs one element per thread:
+    # at 4 per thread it would leave about one wave per SIMD to hide the
+    # latency of every dependent load (measured on the C5 gradient sums:
+    # 196 us vector, 80 us scalar for 2^18 elements and ~75 statements)
+    heavy = n <= SCALAR_MAX_N and sum(1 for k, _ in stmts if k != "tmp") > SCALAR_MIN_STMTS
+    if heavy or not _vector_plan(stmts, n, index_kind, n_cols):
         block = BLOCK
         low = Lowerer(ity, params)
         body = "\n    ".join(low.statements(stmts, init_value))
