@@ -355,3 +355,70 @@ def test_temp_read_through_a_permute_is_reported():
         if not f:
             HIPDevice._check_temps(c)
     ad.reset()
+
+
+# ---------------------------------------------------------------- argument tables
+def _concat_program(pieces):
+    """A concat of ``pieces`` row blocks, scaled: one elementwise plan with
+    a pointer per piece."""
+    import ad_amd as ad
+    from ad_amd.alloc import AllocEntry
+    from ad_amd.graph import Receiver, Tensor
+    ad.reset()
+    rng = np.random.default_rng(3)
+    parts = [Tensor(rng.standard_normal((4, 8)).astype(np.float32)) for _ in range(pieces)]
+    Receiver(lambda v: None, [(ad.concat(parts, 0) * 1.5).contigious()])
+    proc = ad.compile_proc()
+    info = codegen.BufferInfo()
+    for c in proc.procedure:
+        if isinstance(c, AllocEntry):
+            info.size[c.id] = c.size
+    cmds = [c for c in proc.procedure if hasattr(c, "program_id") and type(c).__name__ != "Receiver"]
+    return [p for c in cmds for p in codegen.command_plans(c, info, 0)[0]]
+
+
+def test_table_pointers_are_global_and_many_arguments_are_read_lazily():
+    """Table pointers are cast to the global address space; past LAZY_ARGS
+    arguments the entry point reads each one where the body uses it (no
+    device function taking them all), and the source still compiles."""
+    from ad_amd.device.hip.runtime import HEADER_PATH, compile_source
+    header = pathlib.Path(HEADER_PATH).read_text()
+    few = _concat_program(3)
+    many = _concat_program(codegen.LAZY_ARGS + 6)
+    src_few = next(p.source for p in few if len(p.args) <= codegen.LAZY_ARGS)
+    src_many = next(p.source for p in many if len(p.args) > codegen.LAZY_ARGS)
+    for src in (src_few, src_many):
+        assert "__attribute__((address_space(1)))" in src
+        assert len(compile_source(header + src)) > 0
+    assert "_body(" in src_few and "_body(" not in src_many
+    # every use of an argument reads the table directly
+    assert not re.search(r"\bp\d+\b", src_many.split("tbl_) {", 1)[1])
+
+
+def test_short_heavy_passes_run_one_element_per_thread():
+    """An elementwise pass of at most SCALAR_MAX_N elements with more than
+    SCALAR_MIN_STMTS statements runs one element per thread; a light one or
+    a long one keeps four."""
+    import ad_amd as ad
+    from ad_amd.alloc import AllocEntry
+    from ad_amd.graph import Receiver, Tensor
+
+    def grid(n, ops):
+        ad.reset()
+        x = Tensor(np.ones((n,), np.float32))
+        y = x * 0.5
+        for _ in range(ops - 1):
+            y = y * 1.25 + x
+        Receiver(lambda v: None, [y])
+        proc = ad.compile_proc()
+        info = codegen.BufferInfo()
+        for c in proc.procedure:
+            if isinstance(c, AllocEntry):
+                info.size[c.id] = c.size
+        cmd = next(c for c in proc.procedure if type(c).__name__ == "ElwFuse")
+        (plan,), _, _ = codegen.command_plans(cmd, info, 0)
+        return plan.grid[0] * 256
+    n = codegen.SCALAR_MAX_N
+    assert grid(n, codegen.SCALAR_MIN_STMTS) == n            # threads == elements
+    assert grid(n, 2) * 4 == n
+    assert grid(4 * n, codegen.SCALAR_MIN_STMTS) * 4 == 4 * n

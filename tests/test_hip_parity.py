@@ -418,3 +418,44 @@ def test_bf16_leaves_small_products_fp32(hip):
         ad.execute(device=dev)
         out.append(got["r"])
     assert np.array_equal(out[0], out[1])
+
+
+def test_many_piece_concat_reads_arguments_lazily(hip):
+    """A concat of 40 row blocks (a kernel with more table arguments than it
+    loads at entry) and a DotProd on it, against the oracle."""
+    def build():
+        rng = np.random.default_rng(5)
+        parts = [Tensor(rng.standard_normal((4, 8)).astype(np.float32)) for _ in range(40)]
+        w = Tensor(rng.standard_normal((8, 16)).astype(np.float32))
+        got = {}
+        c = ad.concat(parts, 0)
+        Receiver(lambda a, b: got.update(c=a.copy(), p=b.copy()), [(c * 1.5).contigious(), c @ w])
+        return got
+    ad.reset()
+    a = build()
+    ad.execute(device=hip())
+    ad.reset()
+    b = build()
+    ad.execute(device=OracleDevice())
+    assert np.array_equal(a["c"], b["c"])
+    np.testing.assert_allclose(a["p"], b["p"], rtol=1e-4, atol=1e-5)
+
+
+def test_short_heavy_pass_matches_oracle(hip):
+    """A 2^18-element chain of 15 statements (one element per thread)."""
+    def build():
+        rng = np.random.default_rng(6)
+        x = Tensor(rng.standard_normal((1 << 18,)).astype(np.float32))
+        y = x * 0.5
+        for _ in range(7):
+            y = y * 0.75 + x
+        got = {}
+        Receiver(lambda v: got.update(y=v.copy()), [y])
+        return got
+    ad.reset()
+    a = build()
+    ad.execute(device=hip())
+    ad.reset()
+    b = build()
+    ad.execute(device=OracleDevice())
+    np.testing.assert_allclose(a["y"], b["y"], rtol=1e-5, atol=1e-6)
