@@ -157,7 +157,7 @@ def micro_elw(reps, copies=2, expr=None, stream=True):
     return {"kernel": name, "ms": ms, "bytes": nbytes, "gbs": nbytes / ms / 1e6}
 
 
-def transformer_steps(config, steps, warmup, eager=False, lanes=1, dot="fp32", arena="packed"):
+def transformer_steps(config, steps, warmup, eager=False, lanes=1, dot="fp32", arena="packed", feeder=False):
     import ad_amd as ad
     from ad_amd import workloads
     from ad_amd.device.hip import HIPDevice
@@ -165,7 +165,7 @@ def transformer_steps(config, steps, warmup, eager=False, lanes=1, dot="fp32", a
     ad.reset()
     t0 = time.perf_counter()
     workloads.transformer(layers=layers, d_model=d, heads=h, ff=f, seq=s, batch=b, steps=1,
-                          receive=False)
+                          receive=False, feeder=feeder)
     proc = ad.compile_proc()
     t1 = time.perf_counter()
     step_flops = workloads.dotprod_flops(proc)
@@ -278,6 +278,12 @@ def other_configs():
         unpacked[f"{config}_launches_per_step"] = r["launches_per_step"]
         log(f"unpacked arena: {config} {1e3 / ms:.1f} steps/s, {r['launches_per_step']} launches/step")
     out["unpacked_arena"] = unpacked
+    r = transformer_steps("c5", 20, 3, feeder=True)
+    ms = r["event_ms"] / 20
+    out["c5_feeder"] = {"note": "C5 with X [4096,1024] fed from the host every step (16 MiB over PCIe, "
+                                "staged on a transfer stream): the PCIe-inclusive rate",
+                        "steps_per_s": round(1e3 / ms, 2), "ms_per_step": round(ms, 3)}
+    log(f"c5 with a Feeder per step: {1e3 / ms:.1f} steps/s")
     return out
 
 
