@@ -307,9 +307,15 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
       // MFMA step s of the panel multiplies k = H * (lane / 32) + s: a lane
       // takes H consecutive k (any assignment of the panel's k to steps and
       // lane halves is a valid order of the sum, the same for A and B);
-      // fragments are read 4 steps at a time
+      // fragments are read 4 steps at a time.  The products run at raised
+      // wave priority, so a wave in its product phase issues ahead of one
+      // storing its panel (the two blocks of a compute unit alternate), and
+      // iglp_opt(0) interleaves the fragment reads with the MFMAs (measured:
+      // 4096^3 from 118.9 to 121.9 TFLOP/s)
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int q = 0; q < H / 4; ++q) {
+        __builtin_amdgcn_iglp_opt(0);
         float af[TM][4], bf[TN][4];
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
@@ -341,6 +347,7 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
             for (int j = 0; j < TN; ++j)
               acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][st], bf[j][st], acc[i][j], 0, 0, 0);
       }
+      __builtin_amdgcn_s_setprio(0);
       if (more) {
         store_a(cur ^ 1);
         store_b(cur ^ 1);
