@@ -477,8 +477,10 @@ __device__ __forceinline__ void dp_bf16(const __bf16* __restrict__ A, const __bf
     for (int k0 = kbeg; k0 < kend; k0 += BK) {
       const bool more = k0 + BK < kend;
       if (more) load(k0 + BK);
+      __builtin_amdgcn_s_setprio(1);          // as in dp_mfma
 #pragma unroll
       for (int st = 0; st < BK / 16; ++st) {
+        __builtin_amdgcn_iglp_opt(0);
         adhip_bf16x8 af[TM], bf[TN];
 #pragma unroll
         for (int i = 0; i < TM; ++i)
@@ -492,6 +494,7 @@ __device__ __forceinline__ void dp_bf16(const __bf16* __restrict__ A, const __bf
           for (int j = 0; j < TN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
       }
+      __builtin_amdgcn_s_setprio(0);
       if (more) store(cur ^ 1);
       __syncthreads();
       cur ^= 1;

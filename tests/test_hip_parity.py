@@ -366,7 +366,8 @@ def test_exact_reduce_all_elements(hip, R):
         np.testing.assert_allclose(got[k].reshape(-1), ref[k].reshape(-1), rtol=1e-5, atol=1e-4)
 
 
-@pytest.mark.parametrize("M,K,N", [(256, 512, 128), (300, 200, 130), (1, 3, 1), (130, 70, 257), (64, 4096, 64)])
+@pytest.mark.parametrize("M,K,N", [(256, 512, 128), (300, 200, 130), (1, 3, 1), (130, 70, 257), (64, 4096, 64),
+                                   (520, 1024, 300)])
 @pytest.mark.parametrize("ta,tb", [(False, False), (True, True)])
 def test_bf16_dotprod_bound(hip, M, K, N, ta, tb):
     """dot_precision="bf16" (beyond the reference): operands rounded to
