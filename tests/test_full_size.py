@@ -130,14 +130,15 @@ def _torch_step(res, init, lr=0.01):
 
 
 @gpu
-@pytest.mark.parametrize("config", ["c4", "c5"])
-def test_transformer_step_full_size_vs_torch(hip, config):
+@pytest.mark.parametrize("config,arena", [("c4", "packed"), ("c5", "packed"), ("c4", "unpacked"),
+                                          ("c5", "unpacked")])
+def test_transformer_step_full_size_vs_torch(hip, config, arena):
     layers, d, h, f, s, b = workloads.TRANSFORMER_CONFIGS[config]
     ad.reset()
     res = workloads.transformer(layers=layers, d_model=d, heads=h, ff=f, seq=s, batch=b, steps=1,
                                 receive=False)
     init = {id(p): p.arr.copy() for p in res["params_ref"]}
-    ad.execute(device=hip())
+    ad.execute(device=hip(arena=arena))
     want = _torch_step(res, init)
     for p in res["params_ref"]:
         np.testing.assert_allclose(p.arr, want[id(p)], rtol=1e-4, atol=1e-5)
