@@ -62,6 +62,8 @@ extern "C" __global__ void __launch_bounds__(256) probe_dp_vec_small(float* a) {
 extern "C" __global__ void __launch_bounds__(256) probe_pack(float* a) { adhip::pack_bf16<0>(LA{a}, reinterpret_cast<__bf16*>(a), 64, 64, 64); }
 extern "C" __global__ void __launch_bounds__(256) probe_pack_t(float* a) { adhip::pack_bf16<1>(LB{a}, reinterpret_cast<__bf16*>(a), 64, 64, 64); }
 extern "C" __global__ void __launch_bounds__(256) probe_bf16(float* a) { adhip::dp_bf16<128, 128, 1, 64>(reinterpret_cast<const __bf16*>(a), reinterpret_cast<const __bf16*>(a), 64, EP4{a}, 64, 64); }
+extern "C" __global__ void __launch_bounds__(256) probe_direct(float* a) { adhip::dp_direct(LA{a}, LB{a}, EPI{a}, 64, 64, 2); }
+extern "C" __global__ void __launch_bounds__(256) probe_skinny(float* a) { adhip::dp_skinny<8>(LA{a}, LB{a}, EPI{a}, 2, 64, 64); }
 extern "C" __global__ void __launch_bounds__(256) probe_bf16_w(float* a) { adhip::dp_bf16<256, 128, 2, 32>(reinterpret_cast<const __bf16*>(a), reinterpret_cast<const __bf16*>(a), 64, EP4{a}, 64, 64); }
 extern "C" __global__ void __launch_bounds__(256) probe_bf16_s(float* a) { adhip::dp_bf16<64, 64, 2, 32>(reinterpret_cast<const __bf16*>(a), reinterpret_cast<const __bf16*>(a), 64, EPI{a}, 64, 64); }
 extern "C" __global__ void __launch_bounds__(256) probe_rr(float* a) { adhip::reduce_rows<0>(LD{a}, EPR{a}, 64u, 64u, false); }

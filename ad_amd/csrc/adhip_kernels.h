@@ -359,6 +359,62 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
   dp_epilogue<BM, BN>(epi, acc, smem, m0, n0, M, N, chunk);
 }
 
+// dp_skinny<MR>: a DotProd with at most MR rows (a product like [2,255] x
+// [255,255], where an MFMA tile would idle on the short side and its K
+// panels and barriers would set the time).  A block of 256 lanes takes 16
+// columns; the 16 lanes of a column split K (lane s takes k = s, s + 16,
+// ...), so for K <= 256 a lane has every load in flight at once; the 16
+// partial sums of each row combine by butterfly within the group, and lane
+// s < M of the group runs the epilogue of row s (scalar EPI interface).
+template <int MR, class LA, class LB, class EPI>
+__device__ __forceinline__ void dp_skinny(const LA& la, const LB& lb, const EPI& epi, int M, int N, int K) {
+  const int t = threadIdx.x;
+  const int s = t & 15;
+  const int n = blockIdx.x * 16 + (t >> 4);
+  float acc[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) acc[m] = 0.f;
+  if (n < N) {
+#pragma unroll 4
+    for (int k = s; k < K; k += 16) {
+      const float b = lb.at(k, n);
+#pragma unroll
+      for (int m = 0; m < MR; ++m)
+        if (m < M) acc[m] = acc[m] + la.at(m, k) * b;
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) acc[m] = acc[m] + __shfl_xor(acc[m], off, 16);
+  if (n < N && s < M) {
+    float v = acc[0];
+#pragma unroll
+    for (int m = 1; m < MR; ++m)
+      if (m == s) v = acc[m];
+    constexpr int NL = EPI::kLoads > 0 ? EPI::kLoads : 1;
+    float lv[NL];
+    epi.load(s, n, lv);
+    epi(v, s, n, 0, lv);
+  }
+}
+
+// dp_direct: a DotProd with a short K (at most a few terms, such as the
+// [255,2] x [2,255] weight gradients of a batch of 2): one lane per output,
+// the K products summed in order, then the scalar epilogue; no tile, no LDS.
+template <class LA, class LB, class EPI>
+__device__ __forceinline__ void dp_direct(const LA& la, const LB& lb, const EPI& epi, int M, int N, int K) {
+  const unsigned long long g = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= (unsigned long long)M * (unsigned long long)N) return;
+  const int m = (int)(g / (unsigned long long)N), n = (int)(g % (unsigned long long)N);
+  float acc = 0.f;
+  for (int k = 0; k < K; ++k) acc = acc + la.at(m, k) * lb.at(k, n);
+  constexpr int NL = EPI::kLoads > 0 ? EPI::kLoads : 1;
+  float lv[NL];
+  epi.load(m, n, lv);
+  epi(acc, m, n, 0, lv);
+}
+
 // ---------------------------------------------------------------- bf16 DotProd
 // An option, not the reference: operands rounded to bfloat16 (nearest even),
 // products accumulated in fp32 by v_mfma_f32_32x32x16_bf16.

@@ -1030,7 +1030,7 @@ def epilogue_vec_ok(stmts, M, N) -> bool:
     return N % 4 == 0 and bool(stmts) and _vector_plan(stmts, M * N, "dp", N)
 
 
-def _dp_epi_struct(stmts, params: Params, ity, M, N, partial_off=None) -> str:
+def _dp_epi_struct(stmts, params: Params, ity, M, N, partial_off=None, allow_vec=True) -> str:
     """The ``EPI`` functor of a DotProd kernel: the epilogue statements on
     the product (four consecutive columns per call with float4 accesses when
     every access allows it, else one element per call), or the store of a
@@ -1038,7 +1038,7 @@ def _dp_epi_struct(stmts, params: Params, ity, M, N, partial_off=None) -> str:
     gid = f"const {ity} _global_id = _x * ({ity}){N} + _y; (void)_global_id;"
     if partial_off is not None:
         assert not stmts, "a DotProd storing partial products runs no epilogue"
-    vec4 = N % 4 == 0 and (partial_off is not None or epilogue_vec_ok(stmts, M, N))
+    vec4 = allow_vec and N % 4 == 0 and (partial_off is not None or epilogue_vec_ok(stmts, M, N))
     if vec4:
         if partial_off is not None:
             pp = params.ptr("scratch", 0, partial_off)
@@ -1075,6 +1075,11 @@ def _dp_epi_struct(stmts, params: Params, ity, M, N, partial_off=None) -> str:
             f"    {gid} (void)_chunk; (void)_l;\n    {body}\n  }} }};\n")
 
 
+# products with at most this many rows run ``dp_skinny``, and others with at
+# most this many terms per output ``dp_direct`` (no MFMA tile)
+SKINNY_M, DIRECT_K = 8, 8
+
+
 def dotprod_plan(stmts, dp, A=None, B=None, config=None, partial_off=None) -> KernelPlan:
     """DotProd (+ elementwise epilogue) on fp32 MFMA tiles
     (kernels/dotprod.py:7-43, dp_elw_fuse.py:26-65 semantics).  ``A``/``B``
@@ -1092,6 +1097,19 @@ def dotprod_plan(stmts, dp, A=None, B=None, config=None, partial_off=None) -> Ke
     params = Params()
     la, _ = _loader_struct("LA", A, "A", params, ity, (M, K))
     lb, _ = _loader_struct("LB", B, "B", params, ity, (K, N))
+    if M <= SKINNY_M or K <= DIRECT_K:
+        assert split == 1, "a skinny or short-K DotProd is not split"
+        epi = _dp_epi_struct(stmts, params, ity, M, N, partial_off, allow_vec=False)
+        init = _init_list(params)
+        if M <= SKINNY_M:
+            call, grid = f"adhip::dp_skinny<{SKINNY_M}>", (ceil(N / 16), 1, 1)
+        else:
+            call, grid = "adhip::dp_direct", (ceil(M * N / 256), 1, 1)
+        src = ((la + lb + epi).replace("@FIELDS@", _fields(params)) +
+               f"extern \"C\" __global__ void __launch_bounds__(256) {KNAME}({_params_decl(params)}) {{\n"
+               f"  {call}(LA{{{init}}}, LB{{{init}}}, EPI{{{init}}}, {M}, {N}, {K});\n}}\n")
+        return KernelPlan(src, grid, (256, 1, 1), _plan_args(params), family="dotprod",
+                          flops=2 * M * N * K)
     epi = _dp_epi_struct(stmts, params, ity, M, N, partial_off)
     init = _init_list(params)
     src = ((la + lb + epi).replace("@FIELDS@", _fields(params)) +
@@ -1507,6 +1525,8 @@ def first_pass_plans(part, n, init_node, alloc: ScratchAlloc, opts=DEFAULT_OPTIO
         M, N = init_node.shape
         K = init_node.children_shapes[0][1]
         cfg = dp_config(M, N, K)
+        if M <= SKINNY_M or K <= DIRECT_K:
+            cfg = (cfg[0], cfg[1], 1, cfg[3])
         A, B = init_node.kargs
         if opts.dot == "bf16" and M * N * K >= opts.bf16_min_macs:
             # both operands packed to k-contiguous bf16 in scratch, then the product

@@ -422,3 +422,32 @@ def test_short_heavy_passes_run_one_element_per_thread():
     assert grid(n, codegen.SCALAR_MIN_STMTS) == n            # threads == elements
     assert grid(n, 2) * 4 == n
     assert grid(4 * n, codegen.SCALAR_MIN_STMTS) * 4 == 4 * n
+
+
+def test_products_of_few_rows_use_the_skinny_kernel():
+    """A DotProd of at most SKINNY_M rows compiles to dp_skinny (16 columns
+    per block, never split), one of at most DIRECT_K terms to dp_direct,
+    others to the MFMA tile."""
+    import ad_amd as ad
+    from ad_amd.alloc import AllocEntry
+    from ad_amd.device.hip.runtime import HEADER_PATH, compile_source
+    from ad_amd.graph import Receiver, Tensor
+    header = pathlib.Path(HEADER_PATH).read_text()
+    for M, K, kernel in ((codegen.SKINNY_M, 4096, "dp_skinny"), (codegen.SKINNY_M + 1, 4096, "dp_mfma"),
+                         (300, codegen.DIRECT_K, "dp_direct"), (300, codegen.DIRECT_K + 1, "dp_mfma")):
+        ad.reset()
+        x = Tensor(np.ones((M, K), np.float32))
+        w = Tensor(np.ones((K, 40), np.float32))
+        Receiver(lambda v: None, [(x @ w).sigmoid()])
+        proc = ad.compile_proc()
+        info = codegen.BufferInfo()
+        for c in proc.procedure:
+            if isinstance(c, AllocEntry):
+                info.size[c.id] = c.size
+        cmd = next(c for c in proc.procedure if type(c).__name__ == "DPElwFuse")
+        plans = codegen.command_plans(cmd, info, 0)[0]
+        assert any(kernel in p.source for p in plans)
+        if kernel == "dp_skinny":
+            assert len(plans) == 1 and plans[0].grid == (3, 1, 1)
+        if kernel != "dp_mfma":
+            assert len(compile_source(header + plans[0].source)) > 0

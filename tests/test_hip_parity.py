@@ -36,10 +36,12 @@ def assert_params_close(a, b, rtol=1e-4, atol=1e-5):
         np.testing.assert_allclose(x, y, rtol=rtol, atol=atol)
 
 
-@pytest.mark.parametrize("M,K,N", [(2, 255, 255), (128, 64, 128), (130, 70, 257), (256, 512, 64), (1, 3, 1)])
+@pytest.mark.parametrize("M,K,N", [(2, 255, 255), (128, 64, 128), (130, 70, 257), (256, 512, 64), (1, 3, 1),
+                                   (8, 1000, 300), (5, 17, 64), (9, 40, 33), (300, 2, 200), (64, 8, 130)])
 @pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
 def test_dotprod_shapes(hip, M, K, N, ta, tb):
-    """A @ B through the MFMA template for row-major and transposed
+    """A @ B through the MFMA template (and, for at most 8 rows or at most 8
+    terms, the skinny and direct ones) for row-major and transposed
     operands, against float64 numpy with a K-scaled bound."""
     rng = np.random.default_rng(M * 7 + K * 3 + N)
     a = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
@@ -460,3 +462,27 @@ def test_short_heavy_pass_matches_oracle(hip):
     b = build()
     ad.execute(device=OracleDevice())
     np.testing.assert_allclose(a["y"], b["y"], rtol=1e-5, atol=1e-6)
+
+
+def test_skinny_dotprod_epilogue_and_training(hip):
+    """Products of at most 8 rows (the skinny kernel) with fused epilogues:
+    the C1 MLP (rows of 2) trained 5 steps against the oracle, and
+    sigmoid(A @ B + bias) on [5, 300] x [300, 70] against the oracle."""
+    a, b = run_both(lambda: programs.mlp(steps=5), hip)
+    assert_params_close(a, b)
+
+    def build():
+        rng = np.random.default_rng(11)
+        x = Tensor(rng.standard_normal((5, 300)).astype(np.float32))
+        w = Tensor(rng.standard_normal((300, 70)).astype(np.float32) * 0.05)
+        bias = Tensor(rng.standard_normal((70,)).astype(np.float32))
+        got = {}
+        Receiver(lambda v: got.update(y=v.copy()), [((x @ w) + bias).sigmoid()])
+        return got
+    ad.reset()
+    g = build()
+    ad.execute(device=hip())
+    ad.reset()
+    w = build()
+    ad.execute(device=OracleDevice())
+    np.testing.assert_allclose(g["y"], w["y"], rtol=1e-4, atol=1e-5)
