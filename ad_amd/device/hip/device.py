@@ -232,7 +232,8 @@ class HIPDevice(Device):
         reads and, inside a loop body, that the body itself writes (a range
         the body only reads is read again by the next iteration); a write of
         a range no command reads.  Only ranges of at least
-        ``stream_min_bytes``: the caches keep smaller ones to good effect."""
+        ``stream_min_bytes``: the caches keep smaller ones to good effect.
+        Marks of an earlier device on the same Proc are cleared first."""
         readers, reads, writes = {}, [], []
 
         def nodes(cmd):
@@ -269,7 +270,11 @@ class HIPDevice(Device):
                     if not n.kres.is_none() and not n.kres.is_temp:
                         writes.append((n.kres, codegen._region(n.kres, info)[0]))
         scan(proc, None)
+        for km, _ in reads + writes:
+            km.stream = False
         big = self.stream_min_bytes
+        if big is None:
+            return
         for km, r in reads:
             if len(readers[r]) == 1 and 4 * (r[2] - r[1]) >= big:
                 km.stream = True
@@ -323,8 +328,7 @@ class HIPDevice(Device):
         # kernel plans and the ranges each command touches; commands that need
         # scratch get consecutive slots of a ring, so neighbouring commands do
         # not share scratch and can run in one launch
-        if self.stream_min_bytes is not None:
-            self._mark_streams(proc, info)
+        self._mark_streams(proc, info)
         plans, regions, needs = {}, {}, {}
         for cmd in self._pending:
             if self.strict_temps:

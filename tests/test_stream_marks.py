@@ -76,3 +76,24 @@ def test_results_no_command_reads_are_streamed_on_write():
     Receiver(lambda v: None, [y])
     reads, writes = _marks()
     assert x.id in reads and writes
+
+
+def test_marks_follow_the_device_that_plans():
+    """A second device on the same Proc with streaming off clears the marks
+    the first one left on its accesses."""
+    a = Tensor(np.zeros((64, 64), np.float32))
+    Receiver(lambda v: None, [a.sum(-1) * 0.5])
+    proc = ad.compile_proc()
+    info = codegen.BufferInfo()
+    for c in proc.procedure:
+        if isinstance(c, AllocEntry):
+            info.size[c.id] = c.size
+    marked = []
+    for min_bytes in (1024, None):
+        dev = HIPDevice.__new__(HIPDevice)
+        dev.stream_min_bytes = min_bytes
+        dev._mark_streams(proc, info)
+        marked.append(any(getattr(km, "stream", False) for c in proc.procedure
+                          for n in getattr(c, "nodes", [c]) for k in getattr(n, "kargs", [])
+                          for km in codegen.iter_kmatrix(k)))
+    assert marked == [True, False]
