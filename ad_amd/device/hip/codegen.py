@@ -90,7 +90,7 @@ class KernelPlan:
         return self.name
 
 
-_ENTRY_RE = re.compile(r'extern "C" __global__ void __launch_bounds__\((\d+)\) ' + "adhip_kernel" + r"\(([^)]*)\) \{")
+_ENTRY_RE = re.compile(r'extern "C" __global__ void __launch_bounds__\(([\d, ]+)\) ' + "adhip_kernel" + r"\(([^)]*)\) \{")
 
 
 LAZY_ARGS = 24
@@ -1176,7 +1176,10 @@ def pack_plan(karg, role, rows, K, rows_pad, k_pad, dst_off, dims) -> KernelPlan
 def dotprod_bf16_plan(stmts, dp, a_off, b_off, config, partial_off=None) -> KernelPlan:
     """DotProd (+ epilogue) over operands packed by ``pack_plan`` at scratch
     ``a_off`` / ``b_off``, on bf16 MFMA with fp32 sums; otherwise as
-    ``dotprod_plan``."""
+    ``dotprod_plan``.  The kernel is bounded to two blocks per compute unit:
+    unbounded, the 256 x 128 tile took 156 VGPRs + 128 AGPRs and ran one
+    wave per SIMD (4096^3: 356 TFLOP/s); bounded, 200 registers and two
+    waves (443 TFLOP/s)."""
     M, N = dp.shape
     K = dp.children_shapes[0][1]
     BM, BN, split = config[0], config[1], config[2]
@@ -1189,7 +1192,7 @@ def dotprod_bf16_plan(stmts, dp, a_off, b_off, config, partial_off=None) -> Kern
     epi = _dp_epi_struct(stmts, params, ity, M, N, partial_off)
     init = _init_list(params)
     src = (epi.replace("@FIELDS@", _fields(params)) +
-           f"extern \"C\" __global__ void __launch_bounds__(256) {KNAME}({_params_decl(params)}) {{\n"
+           f"extern \"C\" __global__ void __launch_bounds__(256, 2) {KNAME}({_params_decl(params)}) {{\n"
            f"  adhip::dp_bf16<{BM}, {BN}, {split}, {BF16_PANEL}>(reinterpret_cast<const __bf16*>({pa}), "
            f"reinterpret_cast<const __bf16*>({pb}), {k_pad}, EPI{{{init}}}, {M}, {N});\n}}\n")
     grid = (ceil(N / BN), ceil(M / BM) * split, 1)

@@ -451,3 +451,33 @@ def test_products_of_few_rows_use_the_skinny_kernel():
             assert len(plans) == 1 and plans[0].grid == (3, 1, 1)
         if kernel != "dp_mfma":
             assert len(compile_source(header + plans[0].source)) > 0
+
+
+@pytest.mark.parametrize("M,K,N", [(4096, 4096, 4096), (300, 200, 130)])
+def test_bf16_plans_compile(M, K, N):
+    """The bf16 option's plans (two operand packs, then the product on the
+    256 x 128 tile or the fp32 tile choice, bounded to two blocks per compute
+    unit) compile through hipRTC."""
+    import ad_amd as ad
+    from ad_amd.alloc import AllocEntry
+    from ad_amd.device.hip.runtime import HEADER_PATH, compile_source
+    from ad_amd.graph import Receiver, Tensor
+    header = pathlib.Path(HEADER_PATH).read_text()
+    ad.reset()
+    a = Tensor(np.ones((M, K), np.float32))
+    b = Tensor(np.ones((K, N), np.float32))
+    Receiver(lambda v: None, [(a @ b).sigmoid()])
+    proc = ad.compile_proc()
+    info = codegen.BufferInfo()
+    for c in proc.procedure:
+        if isinstance(c, AllocEntry):
+            info.size[c.id] = c.size
+    cmd = next(c for c in proc.procedure if type(c).__name__ == "DPElwFuse")
+    plans = codegen.command_plans(cmd, info, 0, codegen.PlanOptions(dot="bf16", bf16_min_macs=0))[0]
+    assert [p.family for p in plans][:2] == ["pack", "pack"]
+    product = next(p for p in plans if "dp_bf16" in p.source)
+    assert "__launch_bounds__(256, 2)" in product.source
+    if M >= 256 and N >= 128:
+        assert "dp_bf16<256, 128," in product.source
+    for p in plans:
+        assert len(compile_source(header + p.source)) > 0
