@@ -277,6 +277,10 @@ def other_configs():
         unpacked[f"{config}_steps_per_s"] = round(1e3 / ms, 2)
         unpacked[f"{config}_launches_per_step"] = r["launches_per_step"]
         log(f"unpacked arena: {config} {1e3 / ms:.1f} steps/s, {r['launches_per_step']} launches/step")
+    r = transformer_steps("c5", 20, 3, dot="bf16", arena="unpacked")
+    ms = r["event_ms"] / 20
+    unpacked["c5_bf16_steps_per_s"] = round(1e3 / ms, 2)
+    log(f"unpacked arena and bf16 DotProds: c5 {1e3 / ms:.1f} steps/s")
     out["unpacked_arena"] = unpacked
     r = transformer_steps("c5", 20, 3, feeder=True)
     ms = r["event_ms"] / 20
