@@ -99,3 +99,13 @@ def test_unpacked_random_programs(hip, seed):
     for x, y in zip(got["outs"], ref["outs"]):
         assert x.shape == y.shape
         _close(x, y)
+
+
+def test_unpacked_with_bf16_dotprods(hip):
+    """Both options together (the fastest configuration bench.py reports):
+    a batched transformer trained 3 steps stays within the bf16 tolerance
+    of the fp32 oracle (as test_bf16_training_steps)."""
+    build = BUILDS["batched"]
+    got = _run(build, hip(arena="unpacked", dot_precision="bf16", bf16_min_macs=0))
+    want = _run(build, OracleDevice())
+    assert_params_close(got, want, rtol=2e-3, atol=2e-3)

@@ -57,3 +57,35 @@ def test_an_access_past_the_arena_is_caught(workdir):
     random_program(2002, n_ops=12)
     ok, log = check_run(ad.compile_proc(), workdir, shrink=4)
     assert not ok and "AddressSanitizer" in log
+
+
+@pytest.mark.parametrize("M,K,N", [(520, 1024, 300), (300, 200, 130), (64, 4096, 64), (5, 70, 33)])
+def test_bf16_products_stay_in_bounds(workdir, M, K, N):
+    """The bf16 option's operand packs and products (256 x 128 tiles with
+    padded operands, K splits, the fp32 tile choice below that)."""
+    import numpy as np
+    from ad_amd.graph import Receiver, Tensor
+    rng = np.random.default_rng(M + K + N)
+    a = Tensor(rng.standard_normal((M, K)).astype(np.float32))
+    b = Tensor(rng.standard_normal((N, K)).astype(np.float32))
+    bias = Tensor(rng.standard_normal((N,)).astype(np.float32))
+    Receiver(lambda v: None, [((a @ b.T()) + bias).sigmoid()])
+    ok, log = check_run(ad.compile_proc(), workdir, dot_precision="bf16", bf16_min_macs=0)
+    assert ok, log
+
+
+def test_streamed_accesses_stay_in_bounds(workdir):
+    """Nontemporal float4 accesses (a reduction and a chain over ranges past
+    the streaming threshold, lowered here to 4 KiB)."""
+    import numpy as np
+    from ad_amd.graph import Receiver, Tensor
+    x = Tensor(np.ones((256, 64), np.float32))
+    y = Tensor(np.ones((1 << 12,), np.float32))
+    Receiver(lambda u, v: None, [x.sum(-1) * 0.5, ((y * 0.5 + 1.0).exp2() + 1.0).recip()])
+    ok, log = check_run(ad.compile_proc(), workdir, stream_min_bytes=4096)
+    assert ok, log
+    assert "ld4<true>" in open([f for f in _sources(workdir)][0]).read()
+
+
+def _sources(workdir):
+    return [os.path.join(workdir, f) for f in os.listdir(workdir) if f.endswith(".cpp")]
