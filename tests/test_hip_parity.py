@@ -486,3 +486,35 @@ def test_skinny_dotprod_epilogue_and_training(hip):
     w = build()
     ad.execute(device=OracleDevice())
     np.testing.assert_allclose(g["y"], w["y"], rtol=1e-4, atol=1e-5)
+
+
+def test_feeder_after_receiver_runs_command_by_command(hip):
+    """A loop body that receives a value and then feeds the next one cannot
+    be replayed as a graph (the host callback must run between them): it
+    runs command by command, in the reference's order, and every iteration's
+    received value matches the oracle's (exact in fp32)."""
+    def build():
+        acc = [Tensor(np.zeros((4, 8), np.float32))]
+        seen = []
+        count = [0]
+
+        def feed():
+            count[0] += 1
+            return np.full((4, 8), float(count[0]), np.float32)
+
+        def body():
+            Receiver(lambda v: seen.append(v.copy()), [acc[0]])
+            acc[0] += ad.Feeder(feed, shape=[4, 8])
+        ad.ir_for(range(5), body)
+        return seen
+    ad.reset()
+    got = build()
+    dev = hip()
+    ad.execute(device=dev)
+    assert not dev._graphs
+    ad.reset()
+    want = build()
+    ad.execute(device=OracleDevice())
+    assert len(got) == len(want) == 5
+    for x, y in zip(got, want):
+        assert np.array_equal(x, y)
