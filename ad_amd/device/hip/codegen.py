@@ -739,6 +739,23 @@ def _index_setup(index_kind, ity, n_cols):
 
 
 SCALAR_MAX_N, SCALAR_MIN_STMTS = 1 << 18, 8
+# a longer pass runs one element per thread too when it reads many distinct
+# operands (sums of per-head gradients): measured at 2^22 elements, 16
+# inputs 50 -> 43 us, 48 inputs 173 -> 141 us
+SCALAR_WIDE_MAX_N, SCALAR_WIDE_MIN_LOADS = 1 << 23, 16
+
+
+def _distinct_loads(stmts) -> int:
+    """Distinct memory operands (buffer, access) the statements read."""
+    seen = set()
+    for kind, node in stmts:
+        if kind == "tmp" or not hasattr(node, "kargs"):
+            continue
+        for k in node.kargs:
+            for km in _iter_kmatrix(k):
+                if not km.is_temp:
+                    seen.add((km.id, repr(km.access)))
+    return len(seen)
 
 
 def elementwise_plan(stmts, n, index_kind="global", n_cols=1, flops=0, init_value=None) -> KernelPlan:
@@ -754,7 +771,8 @@ def elementwise_plan(stmts, n, index_kind="global", n_cols=1, flops=0, init_valu
     # at 4 per thread it would leave about one wave per SIMD to hide the
     # latency of every dependent load (measured on the C5 gradient sums:
     # 196 us vector, 80 us scalar for 2^18 elements and ~75 statements)
-    heavy = n <= SCALAR_MAX_N and sum(1 for k, _ in stmts if k != "tmp") > SCALAR_MIN_STMTS
+    heavy = sum(1 for k, _ in stmts if k != "tmp") > SCALAR_MIN_STMTS and (
+        n <= SCALAR_MAX_N or (n <= SCALAR_WIDE_MAX_N and _distinct_loads(stmts) >= SCALAR_WIDE_MIN_LOADS))
     if heavy or not _vector_plan(stmts, n, index_kind, n_cols):
         block = BLOCK
         low = Lowerer(ity, params)
@@ -1415,6 +1433,89 @@ def _stmt_plan(kind, node, n, index_kind, n_cols, temp_off, stage_off, init_off,
                       family="elw")
 
 
+class _Rebound:
+    """A statement node with other operands: every attribute but ``kargs``
+    is the node's own (the Proc is not modified)."""
+
+    def __init__(self, node, kargs):
+        self._node = node
+        self.kargs = kargs
+
+    def __getattr__(self, name):
+        return getattr(self._node, name)
+
+
+# an elementwise read of an arena variable of at most this many floats that a
+# later statement of the same pass overwrites is read from a snapshot copy
+SNAPSHOT_MAX_FLOATS = 1 << 20
+
+
+def _abs_range(km: KMatrix, buffers: BufferInfo):
+    """``[lo, hi)`` of the floats an access may address, in the coordinates
+    of its access expression (the tetris region's for a tetris variable)."""
+    var = getattr(km, "tetris_var", None)
+    if var is not None:
+        return var[1], var[1] + var[2]
+    size = buffers.size.get(km.id)
+    return (0, size) if size is not None else None
+
+
+def snapshot_reads(stmts, pairs, buffers: BufferInfo, scratch_base: int):
+    """Break cross-element conflicts of an elementwise statement list that
+    come from a small operand read by statement ``i`` and overwritten by a
+    later statement ``j`` (a LayerNorm's row means, whose memory the squared
+    deviations reuse): the operand's variable is copied to scratch first and
+    ``i`` reads the copy, so ``i`` and ``j`` can share one pass.  Under the
+    statement-by-statement semantics ``i`` reads the values from before the
+    command, because no statement up to ``i`` writes the variable (else the
+    read is left alone).  Returns ``(statements, copy plans, scratch floats)``
+    or None when nothing is copied."""
+    first_of = {i for i, j in pairs if i < j}
+    writes = []
+    for si, (kind, n) in enumerate(stmts):
+        if kind in ("tmp", "load", "store") or n.kres.is_none() or n.kres.is_temp:
+            continue
+        writes.append((si, _region(n.kres, buffers)[0]))
+    alloc = ScratchAlloc(scratch_base)
+    slots = {}
+    out = list(stmts)
+    for si, (kind, n) in enumerate(stmts):
+        if kind not in ("bin", "un", "copy") or si not in first_of:
+            continue
+        kargs, changed = list(n.kargs), False
+        for ai, k in enumerate(kargs):
+            if not isinstance(k, KMatrix) or k.is_temp or getattr(k, "scratch_offset", None) is not None:
+                continue
+            reg = _region(k, buffers)[0]
+            span = _abs_range(k, buffers)
+            if span is None or span[1] - span[0] > SNAPSHOT_MAX_FLOATS:
+                continue
+
+            def hits(w):
+                return w[0] == reg[0] and w[1] < reg[2] and reg[1] < w[2]
+            if any(wi <= si and hits(w) for wi, w in writes) or not any(wi > si and hits(w) for wi, w in writes):
+                continue
+            if split_const(k.access)[1] < span[0]:
+                continue
+            key = (k.id, span, getattr(k, "tetris_var", None))
+            if key not in slots:
+                slots[key] = alloc.take(span[1] - span[0])
+            km = _scratch_km(slots[key] - span[0], k.access)
+            km.shape = k.shape
+            kargs[ai], changed = km, True
+        if changed:
+            out[si] = (kind, _Rebound(n, kargs))
+    if not slots:
+        return None
+    plans = []
+    for (bid, (lo, hi), var), off in slots.items():
+        src = KMatrix(bid, Add(Val(Global()), Val(Constant(lo))), [hi - lo])
+        if var is not None:
+            src.tetris_var = var
+        plans.append(elementwise_plan([("copy", _Stmt([src], _scratch_km(off, Val(Global()))))], hi - lo))
+    return out, plans, alloc.used
+
+
 # ------------------------------------------------------------------ per-command entry
 def command_plans(cmd, buffers: BufferInfo, scratch_base: int, opts: PlanOptions = DEFAULT_OPTIONS):
     """Plans for one Proc command and the scratch floats they need, under
@@ -1442,10 +1543,19 @@ def command_plans(cmd, buffers: BufferInfo, scratch_base: int, opts: PlanOptions
     plans, end, multipass = [], scratch_base, False
     for group in groups:
         pairs = conflict_pairs(group, buffers, kind, cols)
+        stmts_run, copies, snap = group, [], 0
+        if pairs and init is None and not any(i == j for i, j in pairs):
+            snapped = snapshot_reads(group, pairs, buffers, end)
+            if snapped is not None:
+                cand = conflict_pairs(snapped[0], buffers, kind, cols)
+                if len(split_phases(len(group), cand)) < len(split_phases(len(group), pairs)):
+                    stmts_run, copies, snap = snapped
+                    pairs = cand
         if any(i == j for i, j in pairs):
-            ps, need = lockstep_plans(group, n, kind, cols, init, end, opts)
+            ps, need = lockstep_plans(stmts_run, n, kind, cols, init, end + snap, opts)
         else:
-            ps, need = phased_plans(group, pairs, n, kind, cols, init, end, opts)
+            ps, need = phased_plans(stmts_run, pairs, n, kind, cols, init, end + snap, opts)
+        ps, need = copies + ps, need + snap
         reads, writes = stmt_regions(group, buffers) if len(groups) > 1 else (None, None)
         for p in ps:
             p.reads, p.writes = reads, writes

@@ -424,6 +424,81 @@ def test_short_heavy_passes_run_one_element_per_thread():
     assert grid(4 * n, codegen.SCALAR_MIN_STMTS) * 4 == 4 * n
 
 
+def test_overwritten_small_operand_is_snapshotted_into_one_pass():
+    """The LayerNorm deviation command reads the row means through a
+    broadcast and writes the squared deviations over the means' memory
+    (tetris reuse): the means are copied to scratch first and the two
+    statements share one pass (copy + pass instead of two full passes); the
+    snapshot's read comes from scratch and no statement up to it writes the
+    means."""
+    import ad_amd as ad
+    from ad_amd import workloads
+    from ad_amd.alloc import AllocEntry
+    from ad_amd.graph import ForNode
+    ad.reset()
+    workloads.layernorm_train(rows=256, cols=64, steps=1, receive=False)
+    proc = ad.compile_proc()
+    info = codegen.BufferInfo()
+    for c in proc.procedure:
+        if isinstance(c, AllocEntry):
+            info.size[c.id] = c.size
+    body = next(c for c in proc.procedure if isinstance(c, ForNode)).get_proc()
+    found = False
+    for cmd in body.procedure:
+        if type(cmd).__name__ != "ElwFuse":
+            continue
+        stmts = codegen.statements(cmd.nodes)
+        pairs = codegen.conflict_pairs(stmts, info, "global")
+        snapped = codegen.snapshot_reads(stmts, pairs, info, 0) if pairs else None
+        if snapped is None:
+            continue
+        found = True
+        new, copies, used = snapped
+        assert codegen.conflict_pairs(new, info, "global") == []
+        assert len(copies) == 1 and copies[0].grid[0] * 256 * 4 >= 256 and used >= 256
+        (ps, need, _) = codegen.command_plans(cmd, info, 0)
+        assert len(ps) == 2 and ps[0].grid[0] < ps[1].grid[0] and need == used
+        assert ps[1].grid[0] * 256 * 4 == 256 * 64          # one float4 pass over the elements
+    assert found
+    # the unpacked arena has no such reuse, hence no snapshot
+    info_u = codegen.BufferInfo(unpacked=True)
+    info_u.size = info.size
+    for cmd in body.procedure:
+        if type(cmd).__name__ == "ElwFuse":
+            stmts = codegen.statements(cmd.nodes)
+            assert codegen.conflict_pairs(stmts, info_u, "global") == []
+
+
+def test_wide_passes_of_many_operands_run_one_element_per_thread():
+    """Beyond SCALAR_MAX_N elements, a pass reading at least
+    SCALAR_WIDE_MIN_LOADS distinct operands runs one element per thread (up
+    to SCALAR_WIDE_MAX_N elements); one reading fewer keeps four."""
+    import ad_amd as ad
+    from ad_amd.alloc import AllocEntry
+    from ad_amd.graph import Receiver, Tensor
+
+    def plan(n, inputs):
+        ad.reset()
+        xs = [Tensor(np.ones((n,), np.float32)) for _ in range(inputs)]
+        y = xs[0]
+        for x in xs[1:]:
+            y = y + x
+        Receiver(lambda v: None, [y])
+        proc = ad.compile_proc()
+        info = codegen.BufferInfo()
+        for c in proc.procedure:
+            if isinstance(c, AllocEntry):
+                info.size[c.id] = c.size
+        cmd = next(c for c in proc.procedure if type(c).__name__ == "ElwFuse")
+        (p,), _, _ = codegen.command_plans(cmd, info, 0)
+        return p.grid[0] * 256
+    n = 4 * codegen.SCALAR_MAX_N
+    many = codegen.SCALAR_WIDE_MIN_LOADS
+    assert plan(n, many) == n                                  # threads == elements
+    assert plan(n, many - 1) * 4 == n
+    assert plan(2 * codegen.SCALAR_WIDE_MAX_N, many) * 4 == 2 * codegen.SCALAR_WIDE_MAX_N
+
+
 def test_products_of_few_rows_use_the_skinny_kernel():
     """A DotProd of at most SKINNY_M rows compiles to dp_skinny (16 columns
     per block, never split), one of at most DIRECT_K terms to dp_direct,

@@ -464,6 +464,32 @@ def test_short_heavy_pass_matches_oracle(hip):
     np.testing.assert_allclose(a["y"], b["y"], rtol=1e-5, atol=1e-6)
 
 
+def test_wide_sum_of_many_operands_matches_oracle(hip):
+    """A 2^20-element sum of 20 inputs with a broadcast row factor and two
+    stored partial sums (one element per thread, many operands)."""
+    def build():
+        rng = np.random.default_rng(7)
+        xs = [Tensor(rng.standard_normal((1024, 1024)).astype(np.float32)) for _ in range(20)]
+        w = Tensor(rng.standard_normal((1024,)).astype(np.float32))
+        y = xs[0]
+        parts = []
+        for i, x in enumerate(xs[1:]):
+            y = y + x
+            if i in (9, 18):
+                parts.append(y * w)
+        got = {}
+        Receiver(lambda *v: got.update(v=[a.copy() for a in v]), parts)
+        return got
+    ad.reset()
+    a = build()
+    ad.execute(device=hip())
+    ad.reset()
+    b = build()
+    ad.execute(device=OracleDevice())
+    for u, v in zip(a["v"], b["v"]):
+        np.testing.assert_allclose(u, v, rtol=1e-5, atol=1e-5)
+
+
 def test_skinny_dotprod_epilogue_and_training(hip):
     """Products of at most 8 rows (the skinny kernel) with fused epilogues:
     the C1 MLP (rows of 2) trained 5 steps against the oracle, and
