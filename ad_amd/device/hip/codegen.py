@@ -481,6 +481,8 @@ class _StoreTracker:
         """True if no store so far may have written what ``karg`` reads."""
         if isinstance(karg, KConcat):
             return self.free(karg.karg_one) and self.free(karg.karg_two)
+        if isinstance(karg, KConstant):
+            return True                 # reads nothing
         if not isinstance(karg, KMatrix) or karg.is_temp:
             return False
         if getattr(karg, "scratch_offset", None) is not None:
@@ -567,8 +569,16 @@ class Lowerer:
                 self.hoist = True
             return self._hoisted(expr) or expr
         if isinstance(karg, KConcat):
+            # each piece is read only where the condition selects it: its
+            # access may point outside its buffer for the elements the other
+            # piece serves (a slice read as ``(g % n) - c`` underflows below
+            # c), so no piece's load is hoisted out of the conditional
             cond = lower_index(karg.condition, self.ity)
-            return f"({cond} ? ({self.operand(karg.karg_two)}) : ({self.operand(karg.karg_one)}))"
+            hoist, self.hoist = self.hoist, False
+            try:
+                return f"({cond} ? ({self.operand(karg.karg_two)}) : ({self.operand(karg.karg_one)}))"
+            finally:
+                self.hoist = hoist
         if karg.is_temp:
             return f"temp_{karg.id}"
         p, idx, key = self._loc(karg)

@@ -8,7 +8,10 @@ reported with the kernel that made it.
 Only addresses are checked: every kernel's addresses are functions of its
 indices alone, so cross-lane exchanges and matrix products return their own
 input, barriers do nothing, and the threads of a block run one after
-another.  Test infrastructure; nothing in the package imports it."""
+another.  Loop bodies replay as recorded graphs (with their Feeder staging
+and Receiver snapshot copies), and the argument-table rows each launch
+reads are checked against the table the device wrote.  Test
+infrastructure; nothing in the package imports it."""
 import hashlib
 import os
 import re
@@ -60,18 +63,30 @@ template <class F> static void adhip_launch(F f, const unsigned long long* t, un
 
 
 class RecordingContext:
-    """The ``Context`` calls a device makes before and while it runs a Proc
-    without loops, recorded instead of executed; transfers are checked
-    against the arena."""
+    """The ``Context`` calls a device makes while it prepares and runs a
+    Proc, recorded instead of executed.  Transfers (writes, reads, in-arena
+    copies, staged Feeder copies, Receiver fetches) are checked against the
+    arena; launches are recorded with their grid and argument-table row.
+    Loop bodies are captured into recorded graphs, and every replay of a
+    graph records its launches again, so a loop of n iterations yields n
+    copies of its body's launches, in order."""
 
     def __init__(self):
         self.size = None
         self.base = FAKE_BASE
+        self.h = 1
         self.writes, self.launches, self.errors = [], [], []
+        self._capture = None           # launches of the graph being captured
+        self._graphs = {}
+        self._staging = {}             # tag -> open
+        self._fetch = {}               # set -> (capacity, used, open, pending)
 
     def _check(self, off, n, what):
-        if self.size is None or off < 0 or off + n > self.size:
+        if self.size is None or off < 0 or n < 0 or off + n > self.size:
             self.errors.append((what, off, n, self.size))
+
+    def _sink(self):
+        return self.launches if self._capture is None else self._capture
 
     def reserve(self, n):
         self.size = n
@@ -79,6 +94,8 @@ class RecordingContext:
     def write(self, off, arr):
         arr = np.ascontiguousarray(arr)
         self._check(off, arr.nbytes, "write")
+        if self._capture is not None:
+            self.errors.append(("host write during capture", off, arr.nbytes, self.size))
         self.writes.append((off, arr.tobytes()))
 
     def read(self, off, out):
@@ -87,10 +104,76 @@ class RecordingContext:
     def copy(self, dst, src, n):
         self._check(dst, n, "copy to")
         self._check(src, n, "copy from")
+        if max(dst, src) < min(dst, src) + n:
+            self.errors.append(("overlapping copy", dst, src, n))
+        self._sink().append(("copy", dst, src, n))
 
     def launcher(self, func, grid, block, shared, args):
-        return lambda *_: self.launches.append((func, tuple(grid), tuple(block), args[0]))
+        return lambda *_: self._sink().append(("launch", func, tuple(grid), tuple(block), shared, args[0]))
     launcher_on = launcher
+
+    def graph_begin(self):
+        if self._capture is not None:
+            self.errors.append(("nested capture", 0, 0, self.size))
+        self._capture = []
+
+    def graph_end(self):
+        g = len(self._graphs) + 1
+        self._graphs[g] = self._capture
+        self._capture = None
+        return g
+
+    def graph_launch(self, g):
+        self.launches.extend(self._graphs[g])
+
+    def graph_destroy(self, g):
+        self._graphs.pop(g, None)
+
+    def stage_begin(self, tag):
+        if self._staging.get(tag):
+            self.errors.append(("staging set opened twice", tag, 0, self.size))
+        self._staging[tag] = True
+
+    def stage_write(self, tag, off, arr):
+        if not self._staging.get(tag):
+            self.errors.append(("staged write to a closed set", tag, off, self.size))
+        self._check(off, np.asarray(arr).nbytes, "staged write")
+
+    def stage_end(self, tag):
+        self._staging[tag] = False
+
+    def stage_release(self, tag):
+        pass
+
+    def fetch_reserve(self, fset, nbytes):
+        self._fetch[fset] = [nbytes, 0, False, False]
+
+    def fetch_begin(self, fset):
+        f = self._fetch.get(fset)
+        if f is None or f[2] or f[3]:
+            self.errors.append(("fetch set begun before it was taken", fset, 0, self.size))
+            return
+        f[1], f[2] = 0, True
+
+    def fetch_copy(self, fset, off, nbytes):
+        f = self._fetch[fset]
+        self._check(off, nbytes, "fetch from")
+        host = f[1]
+        f[1] += (nbytes + 255) // 256 * 256
+        if f[1] > f[0]:
+            self.errors.append(("fetch set overflow", fset, f[1], f[0]))
+        return host
+
+    def fetch_end(self, fset):
+        f = self._fetch[fset]
+        f[2], f[3] = False, True
+
+    def fetch_take(self, fset, host_off, out):
+        f = self._fetch[fset]
+        if host_off + out.nbytes > f[1]:
+            self.errors.append(("fetch take out of range", fset, host_off, f[1]))
+        f[3] = False
+        out[...] = 0
 
     def load_module(self, code):
         return code
@@ -98,49 +181,109 @@ class RecordingContext:
     def function(self, mod, name):
         return name
 
-    def fetch_reserve(self, *a): pass
     def lanes_reserve(self, *a): pass
     def sync(self): pass
-    def close(self): pass
     def record_on(self, *a): pass
     def wait_on(self, *a): pass
+
+    def close(self):
+        self.h = None
+
+
+_NARGS_RE = re.compile(r"blockIdx\.z \* (\d+)u")
+
+
+def check_tables(dev, ctx, sources):
+    """Every launch's argument rows lie inside the argument table the device
+    wrote: rows ``row + z * nargs`` for z < grid.z (the kernel's own stride),
+    and every pointer in those rows points into the arena.  No launch asks
+    for dynamic LDS: the kernels declare only static LDS."""
+    errors = []
+    table = [w for w in ctx.writes if w[0] == dev.table_off]
+    if not table:
+        return ["no argument table written"]
+    t_lo, t_hi = dev.table_off, dev.table_off + len(table[-1][1])
+    words = np.frombuffer(table[-1][1], dtype=np.uint64)
+    for op in ctx.launches:
+        if op[0] != "launch":
+            continue
+        _, func, grid, block, shared, row = op
+        m = _NARGS_RE.search(sources[func])
+        nargs = int(m.group(1)) if m else None
+        off = row - FAKE_BASE
+        if nargs is None:
+            errors.append((func, "no table stride in source"))
+            continue
+        if off < t_lo or off + 8 * nargs * grid[2] > t_hi:
+            errors.append((func, "rows outside the table", off, nargs, grid))
+            continue
+        vals = words[(off - t_lo) // 8:(off - t_lo) // 8 + nargs * grid[2]]
+        ptrs = vals[vals >= FAKE_BASE]
+        if ptrs.size and int(ptrs.max()) > FAKE_BASE + ctx.size:
+            errors.append((func, "pointer past the arena", int(ptrs.max()) - FAKE_BASE, ctx.size))
+        if shared and "extern __shared__" not in sources[func]:
+            errors.append((func, "dynamic LDS requested of a kernel without any", shared))
+    return errors
+
+
+def recording_device(**device_options):
+    """A ``HIPDevice`` whose context records (``RecordingContext``) and
+    whose compile step only collects the kernel sources
+    (``dev.recorded_sources``)."""
+    real = devmod.Context
+    devmod.Context = lambda index: RecordingContext()
+    try:
+        dev = devmod.HIPDevice(**device_options)
+    finally:
+        devmod.Context = real
+    dev.recorded_sources = {}
+
+    def record_compile(plans):
+        for ps in plans.values():
+            for p in ps:
+                dev.recorded_sources[p.name] = p.source
+        return {n: n for n in dev.recorded_sources}
+    dev._compile = record_compile
+    return dev
 
 
 def _host_source(src):
     return re.sub(r"__attribute__\(\(address_space\(\d\)\)\)", "", src)
 
 
-def check_run(proc, workdir, shrink=None, **device_options):
-    """Run ``proc`` (no loops) through a recording HIPDevice, then every
-    launch on the host under AddressSanitizer.  ``shrink`` (bytes) cuts the
-    host arena short, to show the check catches an access past it.  Returns
-    ``(ok, log)``."""
-    real = devmod.Context
-    devmod.Context = lambda index: RecordingContext()
-    try:
-        dev = devmod.HIPDevice(use_graphs=False, **device_options)
-    finally:
-        devmod.Context = real
-    sources = {}
-
-    def record_compile(plans):
-        for ps in plans.values():
-            for p in ps:
-                sources[p.name] = p.source
-        return {n: n for n in sources}
-    dev._compile = record_compile
+def check_run(proc, workdir, shrink=None, device=None, **device_options):
+    """Run ``proc`` through a recording HIPDevice (loops replayed as
+    recorded graphs), then check transfers and argument tables
+    (``check_tables``) and run every launch on the host under
+    AddressSanitizer.  ``device`` reuses a recording device (a second
+    program on one device); ``shrink`` (bytes) cuts the host arena short, to
+    show the check catches an access past it.  Returns ``(ok, log)``."""
+    dev = device or recording_device(**device_options)
+    mark = len(dev.ctx.launches)
+    dev.ctx.writes = []
     dev.execute(proc)
     ctx = dev.ctx
+    sources = dev.recorded_sources
     if ctx.errors:
         return False, f"transfers outside the arena: {ctx.errors}"
+    launches = ctx.launches[mark:]
+    saved, ctx.launches = ctx.launches, launches
+    try:
+        bad = check_tables(dev, ctx, sources)
+    finally:
+        ctx.launches = saved
+    if bad:
+        return False, f"argument tables: {bad[:5]}"
     os.makedirs(workdir, exist_ok=True)
     blob = bytearray(ctx.size)
     for off, data in ctx.writes:
         blob[off:off + len(data)] = data
     size = ctx.size - (shrink or 0)
+    used = {op[1] for op in launches if op[0] == "launch"}
     text = [SHIM, _host_source(open(HEADER_PATH).read())]
     for i, (name, src) in enumerate(sources.items()):
-        text.append(f"namespace k{i} {{\n{_host_source(src)}\n}}\nusing k{i}::{name};")
+        if name in used:
+            text.append(f"namespace k{i} {{\n{_host_source(src)}\n}}\nusing k{i}::{name};")
     digest = hashlib.sha1(bytes(blob) + "".join(sources).encode()).hexdigest()[:12]
     blob_path = os.path.join(workdir, f"arena_{digest}.bin")
     with open(blob_path, "wb") as fh:
@@ -152,7 +295,18 @@ def check_run(proc, workdir, shrink=None, **device_options):
     text.append(f"  unsigned long long* tab = (unsigned long long*)(a + {dev.table_off}ull);")
     text.append(f"  for (size_t i = 0; i < {table_words}ull; ++i)"
                 f" if (tab[i] >= {FAKE_BASE}ull) tab[i] = (unsigned long long)(a + (tab[i] - {FAKE_BASE}ull));")
-    for k, (func, grid, block, row) in enumerate(ctx.launches):
+    # one call per distinct launch: replays of a graph repeat the same
+    # addresses, so each (kernel, grid, row) is checked once
+    seen = set()
+    for k, op in enumerate(launches):
+        if op[0] == "copy":
+            _, dst, src, nb = op
+            text.append(f"  memmove(a + {dst}ull, a + {src}ull, {nb}ull);")
+            continue
+        _, func, grid, block, shared, row = op
+        if (func, grid, row) in seen:
+            continue
+        seen.add((func, grid, row))
         text.append(f'  fprintf(stderr, "launch {k} {func}\\n"); adhip_launch({func}, '
                     f"(const unsigned long long*)(a + {row - FAKE_BASE}ull), {grid[0]}, {grid[1]}, {grid[2]}, {block[0]});")
     text.append('  fprintf(stderr, "all launches in bounds\\n");\n  return 0;\n}')

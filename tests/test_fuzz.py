@@ -61,3 +61,21 @@ def test_hip_matches_oracle(hip, seed):
         assert x.shape == y.shape
         _close(x, y)
     ad.reset()
+
+
+@pytest.mark.gpu
+def test_hip_matches_oracle_concat_in_epilogue(hip):
+    """The 12-operation program of seed 2008 with gradients: a DotProd+Elw
+    epilogue reads a concat whose piece index underflows outside the
+    concat's condition (the piece's load stays inside the conditional)."""
+    ad.reset()
+    got, _ = random_program(2008, n_ops=12, grads=True)
+    ad.execute(device=hip())
+    ad.reset()
+    ref, _ = random_program(2008, n_ops=12, grads=True)
+    ad.execute(device=OracleDevice())
+    assert len(got["outs"]) == len(ref["outs"])
+    for x, y in zip(got["outs"], ref["outs"]):
+        assert x.shape == y.shape
+        _close(x, y)
+    ad.reset()

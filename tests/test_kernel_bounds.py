@@ -2,9 +2,10 @@
 the CPU: the device's own plans, arena layout, argument tables and grouped
 launches, run on the host under AddressSanitizer (tests/host_emulation.py).
 Covers random programs (12 operations, forward and gradients, packed and
-unpacked arenas) and the transformer, LayerNorm and MLP steps; a run with
-the host arena cut one float short shows the check catches an access past
-its end."""
+unpacked arenas), the transformer, LayerNorm and MLP training loops (graph
+replay, Feeder staging, in-loop Receivers), several devices in one process
+and a device reused for a second program; a run with the host arena cut
+one float short shows the check catches an access past its end."""
 import os
 import shutil
 
@@ -14,7 +15,7 @@ import ad_amd as ad
 from ad_amd import workloads
 
 from .fuzz_programs import random_program
-from .host_emulation import CLANG, check_run
+from .host_emulation import CLANG, check_run, recording_device
 
 pytestmark = pytest.mark.skipif(not os.path.exists(CLANG), reason="needs the ROCm host clang")
 
@@ -33,24 +34,83 @@ def test_random_programs_stay_in_bounds(workdir, seed, arena):
     assert ok, log
 
 
-@pytest.mark.parametrize("build", ["batched", "layernorm", "mlp"])
-def test_training_steps_stay_in_bounds(workdir, build):
-    builders = {
-        "batched": lambda: workloads.transformer(layers=2, d_model=32, heads=4, ff=64, seq=8, batch=2, steps=1,
-                                                 receive=False),
-        "layernorm": lambda: workloads.layernorm_train(rows=64, cols=1024, steps=1, receive=False),
-        "mlp": lambda: workloads.mlp(steps=1, receive=False),
-    }
-    builders[build]()
-    proc = ad.compile_proc()
-    # the loop body runs once: the emulation replays no graphs
-    from ad_amd.graph import ForNode
-    body = []
-    for c in proc.procedure:
-        body.extend(c.get_proc().procedure if isinstance(c, ForNode) else [c])
-    proc.procedure = body
-    ok, log = check_run(proc, workdir)
+@pytest.mark.parametrize("arena", ["packed", "unpacked"])
+def test_concat_piece_loads_stay_guarded(workdir, arena):
+    """Seed 2008 with gradients: a DotProd epilogue adds a concat whose
+    piece reads a slice as ``(g % 100) - 5``; for g % 100 < 5 that index
+    underflows, and the piece must only be read where the concat's condition
+    selects it.  Its load was hoisted ahead of the condition, an access about
+    16 GiB past the buffer (the GPU sweep's illegal memory access)."""
+    random_program(2008, n_ops=12, grads=True)
+    ok, log = check_run(ad.compile_proc(), workdir, arena=arena)
     assert ok, log
+
+
+_BUILDERS = {
+    "batched": lambda n, r: workloads.transformer(layers=2, d_model=32, heads=4, ff=64, seq=8, batch=2, steps=n,
+                                                  receive=r),
+    "batched_feeder": lambda n, r: workloads.transformer(layers=1, d_model=32, heads=4, ff=64, seq=8, batch=2,
+                                                         steps=n, feeder=True, receive=r),
+    "layernorm": lambda n, r: workloads.layernorm_train(rows=64, cols=1024, steps=n, receive=r),
+    "mlp": lambda n, r: workloads.mlp(steps=n, receive=r),
+}
+
+
+@pytest.mark.parametrize("build", sorted(_BUILDERS))
+def test_training_loops_stay_in_bounds(workdir, build):
+    """Whole programs with their ``ir_for`` loops: bodies captured as graphs
+    and replayed (an unrolled graph plus single ones, Feeder staging slots
+    per iteration), the final Receiver read."""
+    _BUILDERS[build](35, True)
+    ok, log = check_run(ad.compile_proc(), workdir)
+    assert ok, log
+
+
+def _logged_mlp(steps):
+    """A loop body with a Receiver inside (snapshot slots fetched per
+    iteration) and a Feeder before it."""
+    from ad_amd.graph import Feeder, Receiver
+    from ad_amd.nn import Linear, SGD, Sequential, Sigmoid
+    import numpy as np
+    net = Sequential(Linear(16, 24), Sigmoid(), Linear(24, 8))
+    workloads.set_uniform(net.parameters(), 0)
+    opt = SGD(net.parameters(), lr=0.01)
+    x = np.full((2, 16), 0.2, np.float32)
+    seen = []
+
+    def body():
+        opt.zero_grad()
+        out = net(Feeder(lambda: x, shape=[2, 16]))
+        Receiver(lambda v: seen.append(v.copy()), [out.contigious()])
+        out.backward()
+        opt.step()
+    ad.ir_for(range(steps), body)
+    return seen
+
+
+@pytest.mark.parametrize("lag", [0, 1])
+def test_loop_with_receiver_stays_in_bounds(workdir, lag):
+    seen = _logged_mlp(5)
+    ok, log = check_run(ad.compile_proc(), workdir, receiver_lag=lag)
+    assert ok, log
+    assert len(seen) == 5
+
+
+def test_several_devices_and_a_reused_one_stay_in_bounds(workdir):
+    """Devices made and closed one after another in one process, and one
+    device running two programs in turn (its second layout replaces the
+    first's arena, tables and graphs)."""
+    reused = recording_device()
+    for k, seed in enumerate([2000, 2001, 2002]):
+        ad.reset()
+        random_program(seed, n_ops=12, grads=k % 2 == 1)
+        ok, log = check_run(ad.compile_proc(), workdir)
+        assert ok, (seed, log)
+        ad.reset()
+        _BUILDERS["mlp"](3, True) if k % 2 else _BUILDERS["layernorm"](3, True)
+        ok, log = check_run(ad.compile_proc(), workdir, device=reused)
+        assert ok, (seed, "reused device", log)
+    reused.close()
 
 
 def test_an_access_past_the_arena_is_caught(workdir):
