@@ -140,6 +140,19 @@ class HIPDevice(Device):
         self.strict_temps = strict_temps
         self._plan_opts = codegen.PlanOptions(exact_reduce=exact_reduce, dot=dot_precision,
                                               bf16_min_macs=bf16_min_macs)
+        self.jit_threads = jit_threads or min(16, (os.cpu_count() or 4))
+        self.ctx = Context(device_index)
+        self._graphs = {}
+        self._reset_program()
+
+    def _reset_program(self):
+        """Forget every per-program structure: the graphs of an earlier
+        program (destroyed here, after the stream has drained, since they
+        point into the arena the next layout replaces), its layout, plans,
+        slots and schedules.  ``prepare`` starts from here, so one device can
+        run several programs in turn, as the reference's device does by
+        overwriting its dictionaries (device.py:46-91)."""
+        self._destroy_graphs()
         self.kernels = {}            # program_id -> [KernelPlan]
         self.funcs = {}              # program_id -> launch callable (ungrouped)
         self.buffers = {}            # buffer id -> arena byte offset
@@ -147,8 +160,6 @@ class HIPDevice(Device):
         self._vars = {}              # tetris variable id -> (packed float offset, floats)
         self._var_off = {}           # tetris variable id -> arena byte offset (unpacked arena)
         self._events = 0             # event pool entries used by the schedules
-        self.jit_threads = jit_threads or min(16, (os.cpu_count() or 4))
-        self.ctx = Context(device_index)
         self._allocs = []
         self._contents = {}
         self._pending = []
@@ -739,8 +750,9 @@ class HIPDevice(Device):
 
     # ------------------------------------------------------------------ driver
     def prepare(self, proc):
-        """Init pass: layout, upload, JIT, schedules."""
-        self._capturing = False
+        """Init pass: layout, upload, JIT, schedules.  Anything an earlier
+        ``prepare`` of this device built is released first."""
+        self._reset_program()
         self._feeder_size = {}
 
         def note_feeders(c, _):
@@ -783,12 +795,27 @@ class HIPDevice(Device):
             self.ctx.read(self.buffers[bid], out)
             content.reshape(-1)[:] = out
 
-    def close(self):
+    def _destroy_graphs(self):
+        """Destroy the loop graphs once nothing queued can still be running
+        them (a replay returns without waiting)."""
+        if not self._graphs:
+            return
+        self.ctx.sync()
         for singles, unrolled, _, _ in self._graphs.values():
             for g in singles + (unrolled or []):
                 self.ctx.graph_destroy(g)
         self._graphs = {}
-        self.ctx.close()
+
+    def close(self):
+        if getattr(self.ctx, "h", None) is None:
+            return
+        try:
+            self.ctx.sync()
+        finally:
+            try:
+                self._destroy_graphs()
+            finally:
+                self.ctx.close()
 
     def __del__(self):
         try:
