@@ -28,7 +28,8 @@ from .nn import SGD, LayerNorm, Linear, Module, Sequential, Sigmoid
 from .nn.transformer import Attention
 
 __all__ = ["set_uniform", "mlp", "dotprod_elw", "reduce_elw", "elw_chain", "layernorm_train",
-           "BatchedMultiHeadAttention", "BatchedEncoderLayer", "transformer", "TRANSFORMER_CONFIGS"]
+           "BatchedMultiHeadAttention", "BatchedEncoderLayer", "transformer", "TRANSFORMER_CONFIGS",
+           "published_transformer"]
 
 
 def set_uniform(params, seed=0):
@@ -63,16 +64,23 @@ def mlp(steps=1000, din=255, dh=255, dout=255, rows=2, fill=0.2, receive=True):
     return out
 
 
-def dotprod_elw(M=4096, K=4096, N=4096, seed=1):
-    """``sigmoid(A @ B + bias)`` with A, B, bias ~ N(0,1)."""
+def dotprod_elw(M=4096, K=4096, N=4096, seed=1, receive_pre=False):
+    """``sigmoid(A @ B + bias)`` with A, B, bias ~ N(0,1).  With
+    ``receive_pre`` the pre-activation ``A @ B + bias`` is received as well
+    (``out["pre"]``; the same single DotProd+Elw command then also stores
+    it), so a check is not blunted by the sigmoid's saturation."""
     rng = np.random.default_rng(seed)
     a = rng.standard_normal((M, K), dtype=np.float32)
     b = rng.standard_normal((K, N), dtype=np.float32)
     bias = rng.standard_normal((N,), dtype=np.float32)
     A, B, C = Tensor(a), Tensor(b), Tensor(bias)
-    r = ((A @ B) + C).sigmoid()
+    pre = (A @ B) + C
+    r = pre.sigmoid()
     out = {"inputs": (a, b, bias)}
-    Receiver(lambda v: out.setdefault("r", v), [r])
+    if receive_pre:
+        Receiver(lambda v, p: (out.setdefault("r", v), out.setdefault("pre", p)), [r, pre])
+    else:
+        Receiver(lambda v: out.setdefault("r", v), [r])
     return out
 
 
@@ -199,6 +207,28 @@ def transformer(layers=1, d_model=32, heads=4, ff=64, seq=4, batch=1, steps=2, l
     if receive:
         Receiver(lambda *a: res.setdefault("params", [v.copy() for v in a]), opt.parameters)
     return res
+
+
+def published_transformer(layers=1, steps=500, seed=0):
+    """examples/transformer.py:13-39, the configuration README.md:34-45 times:
+    ``TransformerEncoder(num_layers, d_model=64, num_heads=4, ff_dim=128)``,
+    a [2,64] Feeder filled with 0.3 every step, the implicit ``sum`` loss,
+    SGD lr 0.01, ``steps`` iterations in one ``ir_for``.  Weights keep the
+    reference's N(0,1) ``Linear`` init (seeded here)."""
+    from .nn import TransformerEncoder
+    np.random.seed(seed)
+    net = TransformerEncoder(num_layers=layers, d_model=64, num_heads=4, ff_dim=128)
+    opt = SGD(net.parameters(), lr=0.01)
+    x = np.full((2, 64), 0.3, dtype=np.float32)
+
+    def body():
+        opt.zero_grad()
+        net(Feeder(lambda: x, shape=[2, 64])).backward()
+        opt.step()
+    ir_for(range(steps), body)
+    out = {}
+    Receiver(lambda *a: out.setdefault("params", len(a)), opt.parameters)
+    return out
 
 
 def dotprod_flops(proc):

@@ -36,6 +36,30 @@ def test_known_answer_dotprod():
     assert round(float(got["g"].sum()), 4) == 8.2885
 
 
+def _temp_through_permute_program():
+    """``(x*2).T() * y`` in one ElwFuse with y = 1: the product's left
+    operand is the fused temp ``x*2`` read through a transpose."""
+    x = Tensor(np.arange(16, dtype=np.float32).reshape(4, 4))
+    y = Tensor(np.ones((4, 4), dtype=np.float32))
+    got = {}
+    Receiver(lambda v: got.setdefault("v", v.copy()), [((x * 2.0).T() * y).contigious()])
+    return got
+
+
+TEMP_QUIRK_ANSWER = 2.0 * np.arange(16, dtype=np.float32).reshape(4, 4)
+
+
+def test_known_answer_temp_read_through_permute():
+    """The reference lowers a fused temp as ``temp_<id>`` whatever its
+    access (karg.py:47-48), so the transposed read of ``x*2`` inside the
+    fusion yields each element's own ``2*x[i][j]``: by hand, row i is
+    2*(4i, 4i+1, 4i+2, 4i+3), not the transpose 2*(i, i+4, i+8, i+12)."""
+    got = _temp_through_permute_program()
+    run()
+    assert np.array_equal(got["v"], TEMP_QUIRK_ANSWER)
+    assert not np.array_equal(got["v"], TEMP_QUIRK_ANSWER.T)
+
+
 def test_known_answer_unary():
     """reference tests/unary_test.py:11-14"""
     inp = Tensor(np.array([[0.3, 0.2, 0.7, 0.54], [0.13, 0.77, 0.23, 0.22]]), requires_grad=True)
