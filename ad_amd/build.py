@@ -4,7 +4,7 @@ import subprocess
 import sys
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
-SRC = os.path.join(ROOT, "csrc", "adhip.cpp")
+SRCS = [os.path.join(ROOT, "csrc", f) for f in ("adhip.cpp", "adhip_colreduce.cpp")]
 OUT = os.path.join(ROOT, "device", "hip", "libadhip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -14,7 +14,7 @@ FLAGS = ["-O2", "-fPIC", "-shared", "-std=c++17", "--offload-arch=gfx950",
 
 def build_library(verbose=False) -> str:
     tmp = OUT + f".tmp{os.getpid()}"
-    cmd = [HIPCC, *FLAGS, SRC, "-o", tmp, "-lhiprtc"]
+    cmd = [HIPCC, *FLAGS, *SRCS, "-o", tmp, "-lhiprtc"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")

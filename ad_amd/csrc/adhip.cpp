@@ -7,6 +7,8 @@
 #include <hip/hip_runtime.h>
 #include <hip/hiprtc.h>
 
+#include "adhip_internal.h"
+
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -69,6 +71,10 @@ struct adhip_ctx {
   std::vector<hipStream_t> lanes;
   std::vector<hipEvent_t> pool;
   std::vector<adhip_module*> modules;
+  // device memory of library entry points that need scratch (grown on
+  // demand)
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
   std::string err;
 };
 
@@ -100,6 +106,52 @@ int check_range(adhip_ctx* ctx, uint64_t off, size_t bytes) {
 }
 
 }  // namespace
+
+namespace adhip_internal {
+
+hipStream_t stream_of(adhip_ctx* ctx) { return ctx->stream; }
+
+int fail_arg(adhip_ctx* ctx, const char* fmt, ...) {
+  char buf[2048];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  return fail(ctx, ADHIP_E_ARG, "%s", buf);
+}
+
+int fail_state(adhip_ctx* ctx, const char* fmt, ...) {
+  char buf[2048];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  return fail(ctx, ADHIP_E_STATE, "%s", buf);
+}
+
+int fail_hip(adhip_ctx* ctx, hipError_t e, const char* what) {
+  return fail(ctx, (int)e, "%s: %s", what, hipGetErrorString(e));
+}
+
+int workspace(adhip_ctx* ctx, size_t bytes, void** ptr) {
+  if (bytes > ctx->ws_bytes) {
+    if (ctx->capturing) return fail(ctx, ADHIP_E_STATE, "workspace of %zu bytes needed during graph capture", bytes);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    if (ctx->ws) {
+      HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));   // earlier calls may still read it
+      HIP_TRY(ctx, hipFree(ctx->ws));
+      ctx->ws = nullptr;
+      ctx->ws_bytes = 0;
+    }
+    const size_t padded = (bytes + 255) & ~size_t(255);
+    HIP_TRY(ctx, hipMalloc(&ctx->ws, padded));
+    ctx->ws_bytes = padded;
+  }
+  *ptr = ctx->ws;
+  return 0;
+}
+
+}  // namespace adhip_internal
 
 extern "C" {
 
@@ -160,6 +212,7 @@ void adhip_destroy(adhip_ctx* ctx) {
     hipStreamDestroy(st);
   }
   for (auto ev : ctx->pool) hipEventDestroy(ev);
+  if (ctx->ws) hipFree(ctx->ws);
   if (ctx->arena) hipFree(ctx->arena);
   if (ctx->stream) hipStreamDestroy(ctx->stream);
   delete ctx;

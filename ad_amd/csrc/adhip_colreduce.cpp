@@ -1,0 +1,123 @@
+// Column reduction of a row-major [rows, cols] fp32 matrix on caller device
+// memory: out[c] = SUM or MAX over r of x[r * cols + c].  The rows are split
+// into chunks over blocks (the same policy as the generated column
+// reductions: chunks double until there are 512 blocks, at most 128 chunks,
+// at least 64 rows each); each chunk's result goes to a scratch row
+// [chunk][cols], and a second kernel combines the chunks in chunk order.
+//
+// The scratch rows live in device memory the context allocates on first need
+// and keeps (grown when a call needs more) until adhip_destroy.
+#include "../../include/adhip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+
+#include "adhip_kernels.h"
+#include "adhip_internal.h"
+
+namespace {
+
+template <bool V4>
+struct ColLoad {
+  static constexpr bool kVec = false;
+  static constexpr bool kVecX = V4;
+  const float* x;
+  unsigned cols;
+  __device__ float at(unsigned c, unsigned r) const { return x[(size_t)r * cols + c]; }
+  __device__ float4 at4(unsigned c, unsigned r) const {
+    return *reinterpret_cast<const float4*>(x + (size_t)r * cols + c);
+  }
+  __device__ bool inc(unsigned) const { return true; }
+};
+
+struct ToRow {          // chunk results: row `chunk` of [chunks][cols]
+  float* dst;
+  unsigned cols;
+  __device__ void operator()(float v, unsigned c, int chunk) const { dst[(size_t)chunk * cols + c] = v; }
+};
+
+template <int OP, int SPLIT, bool V4>
+__global__ void __launch_bounds__(256) colreduce_chunks(const float* x, float* dst, unsigned rows, unsigned cols) {
+  adhip::reduce_cols<OP, SPLIT>(ColLoad<V4>{x, cols}, ToRow{dst, cols}, cols, rows, false);
+}
+
+template <int OP>
+__global__ void __launch_bounds__(256) colreduce_combine(const float* part, float* out, unsigned chunks, unsigned cols) {
+  const unsigned c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= cols) return;
+  float a = part[c];
+  for (unsigned s = 1; s < chunks; ++s) a = adhip::rop<OP>(a, part[(size_t)s * cols + c]);
+  out[c] = a;
+}
+
+unsigned split_for(unsigned rows, unsigned cols) {
+  const unsigned blocks = (cols + 63) / 64;
+  unsigned split = 1;
+  while (blocks * split < 512 && split < 128 && rows / (2 * split) >= 64) split *= 2;
+  return split;
+}
+
+template <int OP, bool V4>
+hipError_t launch_chunks(unsigned split, const float* x, float* dst, unsigned rows, unsigned cols, hipStream_t st) {
+  const dim3 grid((cols + 63) / 64, split, 1);
+  switch (split) {
+#define ADHIP_CASE(S) \
+  case S: colreduce_chunks<OP, S, V4><<<grid, 256, 0, st>>>(x, dst, rows, cols); break;
+    ADHIP_CASE(1) ADHIP_CASE(2) ADHIP_CASE(4) ADHIP_CASE(8) ADHIP_CASE(16) ADHIP_CASE(32) ADHIP_CASE(64)
+    ADHIP_CASE(128)
+#undef ADHIP_CASE
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// Validates, then enqueues the chunk pass (into `part`, or straight into
+// `out` when there is one chunk) and the combine pass on the context's stream.
+int enqueue(adhip_ctx* ctx, const float* x, float* out, uint32_t rows, uint32_t cols, int op, float* part,
+            unsigned split) {
+  hipStream_t st = adhip_internal::stream_of(ctx);
+  const bool v4 = cols % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+  float* dst = split == 1 ? out : part;
+  hipError_t e;
+  if (op == 0)
+    e = v4 ? launch_chunks<0, true>(split, x, dst, rows, cols, st) : launch_chunks<0, false>(split, x, dst, rows, cols, st);
+  else
+    e = v4 ? launch_chunks<1, true>(split, x, dst, rows, cols, st) : launch_chunks<1, false>(split, x, dst, rows, cols, st);
+  if (e != hipSuccess) return adhip_internal::fail_hip(ctx, e, "column reduction chunk pass");
+  if (split > 1) {
+    const dim3 grid((cols + 255) / 256, 1, 1);
+    if (op == 0) colreduce_combine<0><<<grid, 256, 0, st>>>(part, out, split, cols);
+    else colreduce_combine<1><<<grid, 256, 0, st>>>(part, out, split, cols);
+    e = hipGetLastError();
+    if (e != hipSuccess) return adhip_internal::fail_hip(ctx, e, "column reduction combine pass");
+  }
+  return 0;
+}
+
+int check_args(adhip_ctx* ctx, const float* x, float* out, uint32_t rows, uint32_t cols, int op) {
+  if (!ctx) return adhip_internal::fail_arg(nullptr, "ctx is null");
+  if (op != 0 && op != 1) return adhip_internal::fail_arg(ctx, "op must be 0 (SUM) or 1 (MAX), got %d", op);
+  if (cols && (!x || !out)) return adhip_internal::fail_arg(ctx, "null input or output pointer");
+  if (cols && rows == 0) return adhip_internal::fail_arg(ctx, "a reduction over 0 rows has no value");
+  if ((uint64_t)rows * cols > (1ull << 32)) return adhip_internal::fail_arg(ctx, "rows x cols above 2^32 elements");
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int adhip_reduce_cols(adhip_ctx* ctx, const float* x, float* out, uint32_t rows, uint32_t cols, int op) {
+  if (int r = check_args(ctx, x, out, rows, cols, op)) return r;
+  if (cols == 0) return 0;
+  const unsigned split = split_for(rows, cols);
+  float* part = nullptr;
+  if (split > 1) {
+    if (int rc = adhip_internal::workspace(ctx, (size_t)split * cols * sizeof(float), (void**)&part)) return rc;
+  }
+  return enqueue(ctx, x, out, rows, cols, op, part, split);
+}
+
+}  // extern "C"

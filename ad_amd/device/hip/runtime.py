@@ -23,6 +23,7 @@ EXPORTS = [
     "adhip_module_function", "adhip_launch", "adhip_graph_begin", "adhip_graph_end",
     "adhip_graph_launch", "adhip_graph_destroy", "adhip_sync", "adhip_event_record",
     "adhip_event_elapsed", "adhip_lanes_reserve", "adhip_launch_on", "adhip_record_on", "adhip_wait_on",
+    "adhip_reduce_cols",
 ]
 
 
@@ -75,6 +76,7 @@ def load_library(path=LIB_PATH):
             "adhip_launch_on": (i32, [vp, i32, vp, c.POINTER(u32), c.POINTER(u32), u32, c.POINTER(u64), sz]),
             "adhip_record_on": (i32, [vp, i32, i32]),
             "adhip_wait_on": (i32, [vp, i32, i32]),
+            "adhip_reduce_cols": (i32, [vp, u64, u64, u32, u32, i32]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(lib, name)
@@ -261,6 +263,12 @@ class Context:
         ms = ctypes.c_float()
         self.check(self.lib.adhip_event_elapsed(self.h, a, b, ctypes.byref(ms)), "adhip_event_elapsed")
         return ms.value
+
+    def reduce_cols(self, x_off: int, out_off: int, rows: int, cols: int, op: int = 0):
+        """Column SUM (op 0) or MAX (op 1) of the [rows, cols] matrix at arena
+        byte offset ``x_off`` into ``cols`` floats at ``out_off``."""
+        self.check(self.lib.adhip_reduce_cols(self.h, self.base + x_off, self.base + out_off, rows, cols, op),
+                   "adhip_reduce_cols")
 
     def close(self):
         if self.h:

@@ -135,6 +135,17 @@ void adhip_graph_destroy(adhip_graph* g);
 /* Wait for all queued work.  Replaces clFinish (cl_helper.py:457-458). */
 int  adhip_sync(adhip_ctx* ctx);
 
+/* Column reduction of a row-major [rows, cols] fp32 matrix on device
+ * memory: out[c] = SUM (op 0) or MAX (op 1) over r of x[r * cols + c],
+ * enqueued on the context's stream.  The rows are split into chunks over
+ * blocks; chunk results go to scratch the context allocates on first need
+ * and keeps, and an ordered pass combines them.  Replaces the reduce
+ * kernel (kernels/reduce.py:8-66) for a column reduction such as the
+ * gamma/beta and bias gradients (graph/data/broadcast.py:18-21), with every
+ * row combined (the reference's work-group tree reaches every element for
+ * power-of-two row counts, reduce.py:38-43).  rows >= 1 when cols >= 1. */
+int  adhip_reduce_cols(adhip_ctx* ctx, const float* x, float* out, uint32_t rows, uint32_t cols, int op);
+
 /* Stream events for timing (milliseconds between two recorded events). */
 int  adhip_event_record(adhip_ctx* ctx, int slot);
 int  adhip_event_elapsed(adhip_ctx* ctx, int slot_a, int slot_b, float* ms);

@@ -122,6 +122,17 @@ def test_reference_known_answers_concat_pow2(hip):
     assert np.array_equal(got["s"], np.array([[25, 36, 9, 1], [16, 25, 36, 9]]))
 
 
+def test_reference_known_answer_temp_read_through_permute(hip):
+    """The reference's temp-access rule (karg.py:47-48) by hand: a fused
+    temp read through a transpose yields the element's own value, so
+    ``(x*2).T() * 1`` of x = arange(16) as 4x4 gives 2*x, bit-exact (the
+    oracle's check of the same answer is in test_oracle.py)."""
+    from .test_oracle import TEMP_QUIRK_ANSWER, _temp_through_permute_program
+    got = _temp_through_permute_program()
+    ad.execute(device=hip())
+    assert np.array_equal(got["v"], TEMP_QUIRK_ANSWER)
+
+
 def test_mlp_parity(hip):
     """examples/linear.py (config 1) for 3 SGD steps: every parameter."""
     a, b = run_both(lambda: programs.mlp(steps=3), hip)
@@ -544,3 +555,28 @@ def test_feeder_after_receiver_runs_command_by_command(hip):
     assert len(got) == len(want) == 5
     for x, y in zip(got, want):
         assert np.array_equal(x, y)
+
+
+@pytest.mark.parametrize("rows,cols,op", [(16384, 1024, 0), (3000, 100, 1), (5, 7, 0), (64, 4096, 1)])
+def test_library_column_reduction(rows, cols, op):
+    """adhip_reduce_cols (the C ABI's column SUM / MAX over device memory)
+    against float64 numpy: sums within a sqrt(rows)-scaled bound, maxima
+    exact."""
+    from ad_amd.device.hip.runtime import Context
+    ctx = Context(0)
+    try:
+        x = np.random.default_rng(rows + cols).standard_normal((rows, cols), dtype=np.float32)
+        out_off = 4 * rows * cols + 256
+        ctx.reserve(out_off + 4 * cols + 256)
+        ctx.write(0, x)
+        ctx.reduce_cols(0, out_off, rows, cols, op)
+        got = np.empty(cols, np.float32)
+        ctx.read(out_off, got)
+    finally:
+        ctx.close()
+    if op == 0:
+        want = x.astype(np.float64).sum(0)
+        bound = np.sqrt(rows) * 4 * np.finfo(np.float32).eps * np.abs(x).astype(np.float64).sum(0)
+        assert np.all(np.abs(got - want) <= bound)
+    else:
+        assert np.array_equal(got, x.max(0))
