@@ -72,9 +72,11 @@ struct adhip_ctx {
   std::vector<hipEvent_t> pool;
   std::vector<adhip_module*> modules;
   // device memory of library entry points that need scratch (grown on
-  // demand)
+  // demand), and this device's address of the static scratch array of the
+  // entry points that allocate nothing
   void* ws = nullptr;
   size_t ws_bytes = 0;
+  void* static_scratch = nullptr;
   std::string err;
 };
 
@@ -151,6 +153,8 @@ int workspace(adhip_ctx* ctx, size_t bytes, void** ptr) {
   return 0;
 }
 
+void* static_scratch(adhip_ctx* ctx) { return ctx->static_scratch; }
+
 }  // namespace adhip_internal
 
 extern "C" {
@@ -170,6 +174,13 @@ int adhip_create(int device, adhip_ctx** out) {
     return (int)err;
   };
   if ((e = hipSetDevice(device)) != hipSuccess) return bail(e, "hipSetDevice");
+  // this device's copy of the static scratch array (each device holds its
+  // own, at its own address)
+  if (int rc = adhip_internal::scratch_symbol(device, &ctx->static_scratch)) {
+    g_tls_error = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString((hipError_t)rc);
+    adhip_destroy(ctx);
+    return rc;
+  }
   // default priority, non-blocking w.r.t. the legacy null stream
   if ((e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking)) != hipSuccess)
     return bail(e, "hipStreamCreate");

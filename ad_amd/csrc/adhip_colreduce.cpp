@@ -5,19 +5,33 @@
 // at least 64 rows each); each chunk's result goes to a scratch row
 // [chunk][cols], and a second kernel combines the chunks in chunk order.
 //
-// The scratch rows live in device memory the context allocates on first need
-// and keeps (grown when a call needs more) until adhip_destroy.
+// Two entry points share the kernels and differ only in where the scratch
+// rows live:
+//  * adhip_reduce_cols: device memory the context allocates on first need
+//    and keeps (grown when a call needs more) until adhip_destroy;
+//  * adhip_reduce_cols_noalloc: the file-scope `scratch` array below, whose
+//    per-device address is looked up once per device (hipGetSymbolAddress at
+//    the context's creation); it allocates nothing, so code under graph
+//    capture or a loop that must not allocate can call it.  Every call on
+//    one GPU shares that GPU's array: calls that overlap on one GPU (other
+//    streams, other contexts or threads) race.  Every scratch element a
+//    call reads was written by the same call, so nothing needs clearing.
 #include "../../include/adhip.h"
 
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
 #include <cstring>
+#include <map>
+#include <mutex>
 
 #include "adhip_kernels.h"
 #include "adhip_internal.h"
 
 namespace {
+
+constexpr size_t kScratchFloats = ADHIP_REDUCE_COLS_SCRATCH_FLOATS;
+static __device__ __align__(256) float scratch[kScratchFloats];
 
 template <bool V4>
 struct ColLoad {
@@ -107,6 +121,27 @@ int check_args(adhip_ctx* ctx, const float* x, float* out, uint32_t rows, uint32
 
 }  // namespace
 
+namespace adhip_internal {
+// The address of `scratch` on `device`, which must be current: looked up
+// once per device (hipGetSymbolAddress; each device holds its own copy of
+// the array, at its own address) and kept until the process ends.  Called
+// from adhip_create.
+int scratch_symbol(int device, void** ptr) {
+  static std::mutex lock;
+  static std::map<int, void*> by_device;
+  std::lock_guard<std::mutex> hold(lock);
+  auto it = by_device.find(device);
+  if (it == by_device.end()) {
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    it = by_device.emplace(device, p).first;
+  }
+  *ptr = it->second;
+  return 0;
+}
+}  // namespace adhip_internal
+
 extern "C" {
 
 int adhip_reduce_cols(adhip_ctx* ctx, const float* x, float* out, uint32_t rows, uint32_t cols, int op) {
@@ -116,6 +151,22 @@ int adhip_reduce_cols(adhip_ctx* ctx, const float* x, float* out, uint32_t rows,
   float* part = nullptr;
   if (split > 1) {
     if (int rc = adhip_internal::workspace(ctx, (size_t)split * cols * sizeof(float), (void**)&part)) return rc;
+  }
+  return enqueue(ctx, x, out, rows, cols, op, part, split);
+}
+
+int adhip_reduce_cols_noalloc(adhip_ctx* ctx, const float* x, float* out, uint32_t rows, uint32_t cols, int op) {
+  if (int r = check_args(ctx, x, out, rows, cols, op)) return r;
+  if (cols == 0) return 0;
+  const unsigned split = split_for(rows, cols);
+  if ((size_t)split * cols > kScratchFloats)
+    return adhip_internal::fail_arg(ctx, "adhip_reduce_cols_noalloc: %u chunks x %u columns need %zu scratch floats, "
+                                         "the static scratch holds %zu", split, cols, (size_t)split * cols,
+                                    kScratchFloats);
+  float* part = nullptr;
+  if (split > 1) {
+    part = static_cast<float*>(adhip_internal::static_scratch(ctx));
+    if (!part) return adhip_internal::fail_state(ctx, "static scratch address unknown on this device");
   }
   return enqueue(ctx, x, out, rows, cols, op, part, split);
 }

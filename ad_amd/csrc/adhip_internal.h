@@ -18,6 +18,11 @@ int fail_hip(adhip_ctx* ctx, hipError_t e, const char* what);
 // need, reallocated larger when a call needs more, freed by adhip_destroy).
 // Refused while the context's stream is being captured.
 int workspace(adhip_ctx* ctx, size_t bytes, void** ptr);
+// The context device's address of the column reduction's static scratch
+// array (looked up in adhip_create), or null.
+void* static_scratch(adhip_ctx* ctx);
+// hipGetSymbolAddress of that array on the current device (defined beside it).
+int scratch_symbol(int device, void** ptr);
 }  // namespace adhip_internal
 
 #endif

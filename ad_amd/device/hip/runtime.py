@@ -23,7 +23,7 @@ EXPORTS = [
     "adhip_module_function", "adhip_launch", "adhip_graph_begin", "adhip_graph_end",
     "adhip_graph_launch", "adhip_graph_destroy", "adhip_sync", "adhip_event_record",
     "adhip_event_elapsed", "adhip_lanes_reserve", "adhip_launch_on", "adhip_record_on", "adhip_wait_on",
-    "adhip_reduce_cols",
+    "adhip_reduce_cols", "adhip_reduce_cols_noalloc",
 ]
 
 
@@ -77,6 +77,7 @@ def load_library(path=LIB_PATH):
             "adhip_record_on": (i32, [vp, i32, i32]),
             "adhip_wait_on": (i32, [vp, i32, i32]),
             "adhip_reduce_cols": (i32, [vp, u64, u64, u32, u32, i32]),
+            "adhip_reduce_cols_noalloc": (i32, [vp, u64, u64, u32, u32, i32]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(lib, name)
@@ -269,6 +270,12 @@ class Context:
         byte offset ``x_off`` into ``cols`` floats at ``out_off``."""
         self.check(self.lib.adhip_reduce_cols(self.h, self.base + x_off, self.base + out_off, rows, cols, op),
                    "adhip_reduce_cols")
+
+    def reduce_cols_noalloc(self, x_off: int, out_off: int, rows: int, cols: int, op: int = 0):
+        """``reduce_cols`` with its scratch in the library's static device
+        array: allocates nothing (usable under graph capture)."""
+        self.check(self.lib.adhip_reduce_cols_noalloc(self.h, self.base + x_off, self.base + out_off, rows, cols,
+                                                      op), "adhip_reduce_cols_noalloc")
 
     def close(self):
         if self.h:

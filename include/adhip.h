@@ -31,6 +31,11 @@ typedef struct adhip_graph adhip_graph;
 #define ADHIP_E_COMPILE  1003  /* hipRTC compile failed; log returned */
 #define ADHIP_E_NOTFOUND 1004  /* kernel symbol not found in module */
 
+/* Size of the static scratch array of the column reduction's variant that
+ * allocates nothing: 2^18 floats (1 MiB) per device, held until the process
+ * ends. */
+#define ADHIP_REDUCE_COLS_SCRATCH_FLOATS (1u << 18)
+
 /* Device + stream + pinned staging.  Replaces clGetPlatformIDs /
  * clGetDeviceIDs / clCreateContext / clCreateCommandQueue
  * (cl_helper.py:36-139, device.py:16-51). */
@@ -145,6 +150,17 @@ int  adhip_sync(adhip_ctx* ctx);
  * row combined (the reference's work-group tree reaches every element for
  * power-of-two row counts, reduce.py:38-43).  rows >= 1 when cols >= 1. */
 int  adhip_reduce_cols(adhip_ctx* ctx, const float* x, float* out, uint32_t rows, uint32_t cols, int op);
+/* adhip_reduce_cols without any allocation: the chunk results go to a
+ * static device array of ADHIP_REDUCE_COLS_SCRATCH_FLOATS floats (one per
+ * device, its address looked up once per device when a context is created)
+ * instead of context-owned scratch.  No counterpart in the reference: for
+ * callers that cannot allocate (code under HIP graph capture, serving loops
+ * that forbid hipMalloc).  Same kernels and results as adhip_reduce_cols;
+ * fails with ADHIP_E_ARG when chunks x cols exceed the array (the chunk
+ * count follows the rows, at most 128; see the column reduction source).
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (other streams, contexts or threads) race. */
+int  adhip_reduce_cols_noalloc(adhip_ctx* ctx, const float* x, float* out, uint32_t rows, uint32_t cols, int op);
 
 /* Stream events for timing (milliseconds between two recorded events). */
 int  adhip_event_record(adhip_ctx* ctx, int slot);
