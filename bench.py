@@ -21,11 +21,16 @@
   transformer) at full size, graph-replayed; and the bf16 DotProd option
   (beyond the reference): the 4096^3 DotProd+Elw and the C5 step with
   DotProd operands rounded to bf16.
+* ``value_with_feeder``: the same step with X fed from the host every step
+  (a Feeder; its PCIe upload overlaps the previous step).
 * ``cpu_baseline``: the CPU restatement of the reference OpenCL backend
-  (``oracle``, one OpenMP iteration per work-item, sequential k-loops) timed
-  on this host on a bounded sample of the same workload (the step's FFN
-  DotProd+Elw command on a row slice) and scaled to steps/s by the step's
-  DotProd flops.
+  (``oracle``, one OpenMP iteration per work-item, sequential k-loops, the
+  work-group tree) running real training steps of the same Proc on this
+  host's cores (2 timed steps after an untimed one by default), with the CPU
+  model; ``cpu_other_configs``: C1, C3, C4 and the three single-command
+  benchmarks on the same oracle.
+* ``other_configs.published_config``: examples/transformer.py (the
+  configuration README.md:34-45 times) replayed for 500 and 3000 steps.
 
 Only one GPU is used: ``--gpus`` above 1 exits with a message.
 """
@@ -190,7 +195,7 @@ def transformer_steps(config, steps, warmup, eager=False, lanes=1, dot="fp32", a
     launches = dev.stats["launches_per_iter"]
     dev.close()
     return {"wall_s": t4 - t3, "event_ms": ev_ms, "step_flops": step_flops,
-            "compile_s": t1 - t0, "init_s": t2 - t1, "launches_per_step": launches}
+            "compile_s": t1 - t0, "init_s": t2 - t1, "launches_per_step": launches, "proc": proc}
 
 
 def loop_rate(build, steps, warmup):
@@ -282,56 +287,154 @@ def other_configs():
     unpacked["c5_bf16_steps_per_s"] = round(1e3 / ms, 2)
     log(f"unpacked arena and bf16 DotProds: c5 {1e3 / ms:.1f} steps/s")
     out["unpacked_arena"] = unpacked
-    r = transformer_steps("c5", 20, 3, feeder=True)
-    ms = r["event_ms"] / 20
-    out["c5_feeder"] = {"note": "C5 with X [4096,1024] fed from the host every step (16 MiB over PCIe, "
-                                "staged on a transfer stream): the PCIe-inclusive rate",
-                        "steps_per_s": round(1e3 / ms, 2), "ms_per_step": round(ms, 3)}
-    log(f"c5 with a Feeder per step: {1e3 / ms:.1f} steps/s")
+    out["published_config"] = published_config()
     return out
 
 
-def cpu_baseline(config, step_flops, seconds):
-    """The oracle's work-item kernel for the step's FFN-expand DotProd+Elw
-    (``relu(X @ W1 + b1)``, K = d_model, N = ffn) on a row slice of X,
-    repeated for about ``seconds``; steps/s = flop rate / step DotProd flops
-    (the step's other commands are not charged, so this over-states the CPU)."""
-    import numpy as np
+def host_cpu():
+    """CPU model and the OpenMP threads the oracle runs with (every core of
+    this process's affinity, or OMP_NUM_THREADS if lower)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    cores = len(os.sched_getaffinity(0))
+    threads = min(int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or cores, cores)
+    return model, threads
+
+
+def _oracle(proc):
+    """The CPU restatement of the OpenCL backend with its work-item kernels
+    (one OpenMP iteration per work-item, sequential k-loops, the work-group
+    tree), initialised on ``proc``; returns it and the seconds its kernels
+    took to compile."""
+    from oracle import OracleDevice
+    dev = OracleDevice(lockstep=False)
+    t0 = time.perf_counter()
+    dev._run_proc(proc, dev.init, init=True)
+    dev._finish_init()
+    return dev, time.perf_counter() - t0
+
+
+def oracle_loop(proc, iterations, warmup=1):
+    """Seconds per iteration of the one ``ir_for`` body of ``proc`` on the
+    oracle (``warmup`` untimed iterations first)."""
+    from ad_amd.graph import ForNode
+    dev, jit_s = _oracle(proc)
+    loops = [c for c in proc.procedure if isinstance(c, ForNode)]
+    assert len(loops) == 1
+    inner = loops[0].get_proc()
+    for _ in range(warmup):
+        dev._run_proc(inner, dev.run)
+    t0 = time.perf_counter()
+    for _ in range(iterations):
+        dev._run_proc(inner, dev.run)
+    return (time.perf_counter() - t0) / iterations, jit_s
+
+
+def oracle_command(build, reps):
+    """Seconds per run of the single compute command a builder traces, on
+    the oracle (one untimed run first)."""
+    import ad_amd as ad
+    ad.reset()
+    build()
+    proc = ad.compile_proc()
+    dev, _ = _oracle(proc)
+    cmds = _commands(proc)
+    assert len(cmds) == 1, [type(c).__name__ for c in cmds]
+    fn = dev.funcs[cmds[0].program_id]
+    fn()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    return (time.perf_counter() - t0) / reps
+
+
+def cpu_baseline(proc, config, step_flops, steps=2):
+    """``steps`` real training steps of ``config`` (the Proc the GPU ran) on
+    the oracle's work-item kernels, after one untimed step: the reference's
+    OpenCL execution path restated for the host's cores."""
+    model, threads = host_cpu()
+    sec, jit_s = oracle_loop(proc, steps, warmup=1)
+    log(f"cpu baseline: {config} {sec:.2f} s/step on the oracle ({threads} threads, {model}); "
+        f"kernels compiled in {jit_s:.1f} s")
+    return {"value": round(1.0 / sec, 6), "unit": "steps/s", "cores": threads, "kind": "port",
+            "cpu_model": model,
+            "sample": (f"{steps} {config} training steps (after 1 untimed step) of the oracle's work-item "
+                       f"kernels, the CPU restatement of the reference OpenCL backend, on {threads} "
+                       f"OpenMP threads of {model}: {sec:.2f} s/step, "
+                       f"{step_flops / sec / 1e9:.1f} GFLOP/s of DotProd"),
+            "s_per_step": round(sec, 3)}
+
+
+def cpu_other_configs():
+    """The other configurations and the single-command benchmarks on the
+    oracle: C1 (1000 steps), C3 (5 iterations), C4 (2 steps), the 4096^3
+    DotProd+Elw (1 run), the [8192,4096] Reduce+Elw (10 runs) and the 64 M
+    ElwFuse (5 runs), each after an untimed run."""
     import ad_amd as ad
     from ad_amd import workloads
-    from ad_amd.graph import Receiver, Tensor
-    from oracle import OracleDevice
-    layers, d, h, f, s, b = workloads.TRANSFORMER_CONFIGS[config]
-    rows = 128
+    model, threads = host_cpu()
+    out = {"cpu_model": model, "cores": threads}
     ad.reset()
-    rng = np.random.default_rng(1)
-    x = Tensor(rng.standard_normal((rows, d), dtype=np.float32))
-    w = Tensor(rng.uniform(-1 / d ** 0.5, 1 / d ** 0.5, (d, f)).astype(np.float32))
-    bias = Tensor(rng.uniform(-1 / d ** 0.5, 1 / d ** 0.5, (f,)).astype(np.float32))
-    Receiver(lambda v: None, [((x @ w) + bias).relu()])
+    workloads.mlp(steps=1, receive=False)
+    sec, _ = oracle_loop(ad.compile_proc(), 1000, warmup=10)
+    out["c1_mlp"] = {"us_per_step": round(sec * 1e6, 1), "steps_per_s": round(1 / sec, 1)}
+    ad.reset()
+    workloads.layernorm_train(rows=16384, cols=1024, steps=1, receive=False)
+    sec, _ = oracle_loop(ad.compile_proc(), 5)
+    out["c3_layernorm"] = {"ms_per_iter": round(sec * 1e3, 2), "proc_gbs": round(C3_PROC_BYTES / sec / 1e9, 1)}
+    layers, d, h, f, s, b = workloads.TRANSFORMER_CONFIGS["c4"]
+    ad.reset()
+    workloads.transformer(layers=layers, d_model=d, heads=h, ff=f, seq=s, batch=b, steps=1, receive=False)
+    sec, _ = oracle_loop(ad.compile_proc(), 2)
+    out["c4_transformer"] = {"steps_per_s": round(1 / sec, 3), "s_per_step": round(sec, 3)}
+    sec = oracle_command(lambda: workloads.dotprod_elw(4096, 4096, 4096), 1)
+    out["dotprod_elw_4096"] = {"s": round(sec, 3), "tflops": round(2 * 4096 ** 3 / sec / 1e12, 4)}
+    sec = oracle_command(lambda: workloads.reduce_elw(8192, 4096, 0.5), 10)
+    out["reduce_elw_8192x4096"] = {"ms": round(sec * 1e3, 2), "gbs": round((4 * 8192 * 4096 + 4 * 8192) / sec / 1e9, 1)}
+    sec = oracle_command(lambda: workloads.elw_chain(64 << 20), 5)
+    out["elw_fuse_64m"] = {"ms": round(sec * 1e3, 2), "gbs": round(2 * 4 * (64 << 20) / sec / 1e9, 1)}
+    log(f"cpu: c1 {out['c1_mlp']['us_per_step']} us/step, c3 {out['c3_layernorm']['ms_per_iter']} ms/iter, "
+        f"c4 {out['c4_transformer']['s_per_step']} s/step, dotprod {out['dotprod_elw_4096']['tflops']} TFLOP/s, "
+        f"reduce {out['reduce_elw_8192x4096']['gbs']} GB/s, elw {out['elw_fuse_64m']['gbs']} GB/s")
+    return out
+
+
+def published_config():
+    """examples/transformer.py (1 layer, d_model 64, 4 heads, ff 128, [2,64]
+    Feeder per step) replayed for 500 and 3000 steps: README.md:34-36 times
+    this configuration at 1.32 s (1 layer, CUDA backend on an A100; the step
+    count is not stated; the script runs 500, the screenshot's torch run
+    3000)."""
+    import ad_amd as ad
+    from ad_amd import workloads
+    from ad_amd.device.hip import HIPDevice
+    ad.reset()
+    workloads.published_transformer(layers=1, steps=1)
     proc = ad.compile_proc()
-    dev = OracleDevice(lockstep=False)
-    dev.execute(proc)                         # compiles and runs once (warm-up)
-    cmds = _commands(proc)
-    assert len(cmds) == 1
-    fn = dev.funcs[cmds[0].program_id]
-    n = 0
-    t0 = time.perf_counter()
-    while True:
-        fn()
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    flops = n * 2 * rows * d * f
-    rate = flops / el
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or len(os.sched_getaffinity(0))
-    threads = min(threads, len(os.sched_getaffinity(0)))
-    return {"value": rate / step_flops, "unit": "steps/s", "cores": threads, "kind": "port",
-            "sample": (f"{n} runs of the step's FFN DotProd+Elw relu(X@W1+b1) on a [{rows},{d}]x[{d},{f}] "
-                       f"row slice ({el:.1f} s, {rate / 1e9:.1f} GFLOP/s on the CPU oracle), scaled by "
-                       f"{step_flops / 1e12:.3f} TFLOP of DotProd per step; other commands not charged"),
-            "gflops": rate / 1e9}
+    dev = HIPDevice()
+    dev.prepare(proc)
+    loop = dev.loops(proc)[0]
+    dev.replay(loop, 32)
+    dev.ctx.sync()
+    out = {"workload": "examples/transformer.py: TransformerEncoder(1 layer, d_model 64, 4 heads, ff 128), "
+                       "[2,64] Feeder of 0.3 per step, SGD lr 0.01",
+           "readme_seconds": 1.32, "launches_per_step": dev.stats["launches_per_iter"]}
+    for steps in (500, 3000):
+        t0 = time.perf_counter()
+        dev.replay(loop, steps)
+        dev.ctx.sync()
+        out[f"seconds_{steps}_steps"] = round(time.perf_counter() - t0, 4)
+    dev.close()
+    log(f"published config: 500 steps {out['seconds_500_steps']} s, 3000 steps {out['seconds_3000_steps']} s "
+        f"(README: 1.32 s)")
+    return out
 
 
 def main():
@@ -341,7 +444,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c5", choices=["c4", "c5"])
     ap.add_argument("--micro-reps", type=int, default=20)
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-steps", type=int, default=2, help="timed training steps of the CPU baseline")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-micro", action="store_true", help="skip the single-command benchmarks")
     ap.add_argument("--no-configs", action="store_true", help="skip the C1/C3/C4 measurements")
@@ -396,14 +499,23 @@ def main():
     ms_per_step = tr["wall_s"] * 1e3 / args.steps
     log(f"{args.config}: {ms_per_step:.2f} ms/step wall, {tr['event_ms'] / args.steps:.2f} ms/step "
         f"events, {value:.3f} steps/s, {tr['launches_per_step']} launches/step")
+    # the same step with X fed from the host every step (a Feeder: the
+    # [B*S, d_model] input crosses PCIe on a transfer stream while the
+    # previous step computes), timed the same way
+    fd = transformer_steps(args.config, args.steps, args.warmup, eager=args.eager, lanes=args.lanes,
+                           arena=args.arena, feeder=True)
+    fd.pop("proc")
+    feeder_value = args.steps / fd["wall_s"]
+    log(f"{args.config} with a Feeder per step: {fd['wall_s'] * 1e3 / args.steps:.2f} ms/step wall, "
+        f"{feeder_value:.3f} steps/s")
 
     others = None if args.no_configs else other_configs()
 
-    cpu = None
+    cpu = cpu_others = None
     if not args.no_cpu:
-        cpu = cpu_baseline(args.config, tr["step_flops"], args.cpu_seconds)
-        log(f"cpu baseline: {cpu['value']:.5f} steps/s ({cpu['gflops']:.1f} GFLOP/s, {cpu['cores']} threads)")
-        cpu.pop("gflops")
+        cpu = cpu_baseline(tr["proc"], args.config, tr["step_flops"], args.cpu_steps)
+        cpu_others = None if args.no_configs else cpu_other_configs()
+    tr.pop("proc")
 
     layers, d, h, f, s, b = __import__("ad_amd.workloads", fromlist=["x"]).TRANSFORMER_CONFIGS[args.config]
     roofline = None
@@ -425,10 +537,15 @@ def main():
                                + (", unpacked arena" if args.arena == "unpacked" else ""),
                    "layers": layers, "d_model": d, "heads": h, "ffn": f, "seq_len": s, "batch": b,
                    "parallelism": "none (1 GPU)"},
+        "value_with_feeder": {"value": round(feeder_value, 4), "unit": "steps/s",
+                              "ms_per_step": round(fd["wall_s"] * 1e3 / args.steps, 3),
+                              "note": "the same step with X fed from the host each step by a Feeder "
+                                      "(PCIe upload overlapped with the previous step)"},
         "step_dotprod_tflops": round(tr["step_flops"] / (ms_per_step * 1e9), 2),
         "launches_per_step": tr["launches_per_step"],
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "cpu_other_configs": cpu_others,
         "microbench": micro or None,
         "other_configs": others,
     }

@@ -317,6 +317,48 @@ def kernel_source(cmd, name, exact_reduce=False):
     raise TypeError(f"Encountered unexpected cmd: {cmd}")
 
 
+def work_item_only(source: str, name: str) -> str:
+    """The ``<name>_wi`` function of a command's source (each generator
+    emits the lockstep function ``<name>`` first, then ``<name>_wi``)."""
+    i = source.index(f'extern "C" void {name}_wi(')
+    return source[i:]
+
+
+def compile_cpp_parallel(sources, jobs: int) -> str:
+    """Compile the functions ``sources`` (texts without the prelude) in
+    ``jobs`` translation units at once and link them into one cached shared
+    object; returns its path.  For the work-item kernels of whole training
+    steps (thousands of commands), which one g++ run takes minutes over."""
+    os.makedirs(_CACHE, exist_ok=True)
+    flags = ["-O3", "-march=native", "-ffp-contract=off", "-fno-math-errno", "-fPIC", "-w", "-fopenmp"]
+    key = hashlib.sha256(("".join(sources) + " ".join(flags)).encode()).hexdigest()[:24]
+    so = os.path.join(_CACHE, f"p_{key}.so")
+    if os.path.exists(so):
+        return so
+    jobs = max(1, min(jobs, len(sources)))
+    parts, sizes = [[] for _ in range(jobs)], [0] * jobs
+    for src in sorted(sources, key=len, reverse=True):
+        j = sizes.index(min(sizes))
+        parts[j].append(src)
+        sizes[j] += len(src)
+    procs, objs = [], []
+    for j, part in enumerate(parts):
+        path = os.path.join(_CACHE, f"p_{key}_{j}.cpp")
+        with open(path, "w") as fh:
+            fh.write(_PRELUDE + "".join(part))
+        objs.append(path + f".o{os.getpid()}")
+        procs.append(subprocess.Popen(["g++", *flags, "-c", path, "-o", objs[-1]]))
+    bad = [p.wait() for p in procs]
+    if any(bad):
+        raise RuntimeError(f"g++ failed on {sum(1 for b in bad if b)} of {jobs} parts")
+    tmp = so + f".tmp{os.getpid()}"
+    subprocess.run(["g++", "-shared", "-fopenmp", *objs, "-o", tmp], check=True)
+    os.replace(tmp, so)
+    for o in objs:
+        os.remove(o)
+    return so
+
+
 def compile_cpp(source: str, threads_flag=True) -> str:
     """Compile ``source`` into a cached shared object and return its path."""
     os.makedirs(_CACHE, exist_ok=True)
@@ -340,7 +382,8 @@ class OracleDevice:
     the CPU.  Buffers are numpy float32 arrays; a Tensor's buffer IS its
     ``arr`` (the reference uses CL_MEM_USE_HOST_PTR on a CPU device)."""
 
-    def __init__(self, feeder_offset_zero=False, threads=None, lockstep=True, exact_reduce=False):
+    def __init__(self, feeder_offset_zero=False, threads=None, lockstep=True, exact_reduce=False, jobs=None):
+        self.jobs = jobs
         self.kernels = {}
         self.exact_reduce = exact_reduce
         self.funcs = {}
@@ -387,8 +430,14 @@ class OracleDevice:
     def _finish_init(self):
         if not self._pending:
             return
-        source = _PRELUDE + "".join(p[3] for p in self._pending)
-        self._lib = ctypes.CDLL(compile_cpp(source))
+        if self.lockstep:
+            self._lib = ctypes.CDLL(compile_cpp(_PRELUDE + "".join(p[3] for p in self._pending)))
+        else:
+            # work-item kernels only, compiled in parallel (the timed CPU
+            # baseline of whole training steps)
+            jobs = self.jobs or len(os.sched_getaffinity(0))
+            self._lib = ctypes.CDLL(compile_cpp_parallel(
+                [work_item_only(p[3], p[1]) for p in self._pending], jobs))
         for pid, name, args, _ in self._pending:
             fn = getattr(self._lib, name if self.lockstep else name + "_wi")
             fn.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
