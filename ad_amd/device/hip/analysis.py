@@ -82,6 +82,13 @@ def upper_bound(e, gmax=0, xmax=0, ymax=0):
     return _bounds(e, gmax, xmax, ymax)[1]
 
 
+def interval(e, gmax=0, xmax=0, ymax=0):
+    """``(lo, hi)``: smallest and largest value ``e`` can take for Global,
+    X, Y in ``[0, gmax]``, ``[0, xmax]``, ``[0, ymax]`` (non-negative
+    semantics: a difference is bounded below by 0)."""
+    return _bounds(e, gmax, xmax, ymax)
+
+
 def _bounds(e, gmax, xmax, ymax):
     c = const_of(e)
     if c is not None:

@@ -32,10 +32,11 @@ from ...alloc import AllocEntry
 from ...expr import (Add, BitwiseAnd, Constant, Div, Global, LessThan, Minus, MoreThan, Mult,
                      Remainder, ShiftLeft, ShiftRight, Val, X, Y)
 from ...fusion import DPElwFuse, ElwFuse, ReduceElwFuse
-from ...graph import (BinaryNode, BinaryOp, ContigiousNode, DotProdNode, ReduceNode, ReduceOp,
+from ...graph import (BinaryNode, BinaryOp, ContigiousNode, DotProdNode, Receiver, ReduceNode, ReduceOp,
                       UnaryNode, UnaryOp)
 from ...kernalize import KConcat, KConstant, KMatrix
-from .analysis import AFF, INV, const_of, split_const, upper_bound, vec_class
+from ...node import Node
+from .analysis import AFF, INV, const_of, interval, split_const, upper_bound, vec_class
 
 BLOCK = 256
 _TEMP_RE = re.compile(r"\btemp_\d+\b")
@@ -180,6 +181,85 @@ class BufferInfo:
         self.unpacked = unpacked
 
 
+def access_span(km: KMatrix, domain):
+    """Floats ``[lo, hi)`` of its buffer that an access can touch, given
+    the index space ``domain`` of the operand's role (Global below
+    prod(domain); X, Y below its first and second extent): interval bounds
+    of the access expression.  A subtraction that could go below zero is
+    bounded below by 0: a concat piece is read only where its condition
+    holds, and there its index is a valid one."""
+    n = 1
+    for d in domain:
+        n *= int(d)
+    if n <= 0:
+        return None
+    xmax = int(domain[0]) - 1
+    ymax = int(domain[1]) - 1 if len(domain) > 1 else 0
+    lo, hi = interval(km.access, n - 1, xmax, ymax)
+    return lo, hi + 1
+
+
+def _note_span(karg, domain):
+    for km in _iter_kmatrix(karg):
+        if km.is_temp:
+            continue
+        sp = access_span(km, domain)
+        if sp is None:
+            continue
+        old = getattr(km, "span", None)
+        km.span = sp if old is None else (min(old[0], sp[0]), max(old[1], sp[1]))
+
+
+def annotate_spans(proc):
+    """Record on every buffer access of a Proc (``km.span``) the floats it
+    can touch, from its access expression and the index space of its role:
+    a DotProd's operands range over [M, K] and [K, N] and its result over
+    [M, N] (X, Y); a Reduce's operand over [V, R] and its result over [V];
+    an elementwise statement, Feeder or Receiver over its shape (Global).
+
+    This is what the reference's tetris pass leaves to go on
+    (alloc/tetris_opt.py:159-188 rewrites every access of an arena variable
+    to ``expr + offset`` on the shared region without recording which
+    variable it was): every float an access touches lies in its span, so
+    accesses whose spans do not overlap cannot conflict, and scheduling and
+    hazard analysis stay as fine as the accesses themselves.  Spans are
+    cleared and recomputed on every call."""
+    from ...graph import ForNode
+    todo = []
+
+    def walk(p):
+        for c in p.procedure:
+            if isinstance(c, ForNode):
+                walk(c.get_proc())
+            elif hasattr(c, "nodes"):
+                todo.extend(n for n in c.nodes if isinstance(n, Node))
+            elif isinstance(c, Node):
+                todo.append(c)
+    walk(proc)
+    for n in todo:
+        for k in list(n.kargs) + ([n.kres] if n.kres is not None and not n.kres.is_none() else []):
+            for km in _iter_kmatrix(k):
+                km.span = None
+    for n in todo:
+        if isinstance(n, DotProdNode):
+            _note_span(n.kargs[0], n.children_shapes[0])
+            _note_span(n.kargs[1], n.children_shapes[1])
+            if not n.kres.is_none():
+                _note_span(n.kres, n.shape)
+        elif isinstance(n, ReduceNode):
+            _note_span(n.kargs[0], n.children_shapes[0])
+            if not n.kres.is_none():
+                _note_span(n.kres, n.shape)
+        elif isinstance(n, Receiver):
+            for k in n.kargs:
+                _note_span(k, k.shape)
+        else:                       # elementwise statements, copies, Feeders
+            for k in n.kargs:
+                _note_span(k, n.shape)
+            if n.kres is not None and not n.kres.is_none():
+                _note_span(n.kres, n.shape)
+
+
 def _region(km: KMatrix, buffers: BufferInfo):
     var = getattr(km, "tetris_var", None)
     if var is not None:
@@ -187,6 +267,9 @@ def _region(km: KMatrix, buffers: BufferInfo):
         if buffers.unpacked:
             return (("tv", vid), 0, size), vid
         return (km.id, off, off + size), vid
+    span = getattr(km, "span", None)
+    if span is not None:
+        return (km.id, span[0], span[1]), ("buf", km.id)
     return (km.id, 0, buffers.size.get(km.id, 1 << 62)), ("buf", km.id)
 
 

@@ -760,6 +760,7 @@ class HIPDevice(Device):
                 self._feeder_size[c.id] = prod(c.shape)
             return c
         proc.walk(note_feeders, step_fused=False, step_proc=True)
+        codegen.annotate_spans(proc)
         self._run_proc(proc, self.init, init=True)
         self._finish_init(proc)
         for loop in self.loops(proc):
