@@ -1,41 +1,27 @@
-"""Allocation planning: Alloc/Dealloc insertion, register temps, the
-"tetris" arena packer and hoisting (autodiff/alloc/)."""
-from dataclasses import dataclass
-from typing import Optional
+"""Allocation planning of a linearized Proc (autodiff/alloc/__init__.py:59-76):
 
-__all__ = ["LocationBase", "Location", "AllocCmds", "AllocEntry", "DeallocEntry", "alloc"]
+1. ``insert_alloc`` -- an ``AllocEntry`` before each buffer's first
+   definition and a ``DeallocEntry`` after its last read;
+2. ``temp_alloc`` -- buffers born and dead inside one fused group become
+   register temps;
+3. ``tetris_opt`` -- the remaining buffers of each Proc are packed into one
+   shared region by lifetime;
+4. ``temp_clean`` -- leftover allocations hoisted to the front, releases to
+   the end.
 
+The entries print as the reference's listings show them."""
 
-@dataclass
-class LocationBase:
-    fused_id: Optional[int]
-    proc_id: Optional[int]
-
-    def __hash__(self):
-        return hash((self.fused_id, self.proc_id))
-
-
-@dataclass
-class Location:
-    loc: int
-    fused_id: Optional[int]
-    proc_id: Optional[int]
-
-    def __add__(self, other):
-        if type(other) == int:
-            return Location(self.loc + other, fused_id=self.fused_id, proc_id=self.proc_id)
-        raise TypeError(f"Invalid type for add loc: {type(other)}")
-
-    def base(self) -> LocationBase:
-        return LocationBase(fused_id=self.fused_id, proc_id=self.proc_id)
+__all__ = ["AllocCmds", "AllocEntry", "DeallocEntry", "alloc"]
 
 
 class AllocCmds:
-    pass
+    """Marker base of the allocation commands in a Proc."""
 
 
 class AllocEntry(AllocCmds):
-    """Buffer ``id`` of ``size`` floats; ``content`` is a Tensor's host data."""
+    """Buffer ``id`` of ``size`` floats; ``content`` is the host array of a
+    Tensor it is initialised from, if any; ``is_temp`` marks a register temp
+    of a fused group."""
 
     def __init__(self, alloc_id: int, size: int, content=None):
         self.id = alloc_id
@@ -44,30 +30,31 @@ class AllocEntry(AllocCmds):
         self.is_temp = False
 
     def __repr__(self):
-        head = "TEMP Alloc" if self.is_temp else "Alloc"
-        size = "" if self.is_temp else f" {self.size}"
-        return f"{head} {self.id}{size}" + (" (has content)" if self.content is not None else "")
+        if self.is_temp:
+            text = f"TEMP Alloc {self.id}"
+        else:
+            text = f"Alloc {self.id} {self.size}"
+        return text + (" (has content)" if self.content is not None else "")
 
 
 class DeallocEntry(AllocCmds):
+    """Release of buffer ``id`` (``size`` floats)."""
+
     def __init__(self, dealloc_id: int, size: int):
         self.id = dealloc_id
         self.size = size
         self.is_temp = False
 
     def __repr__(self):
-        return f"{'TEMP ' if self.is_temp else ''}Dealloc {self.id} {self.size}"
+        return ("TEMP " if self.is_temp else "") + f"Dealloc {self.id} {self.size}"
 
 
 def alloc(proc):
-    """insert_alloc -> temp_alloc -> tetris_opt -> temp_clean
-    (alloc/__init__.py:59-76)."""
     from .clean import temp_clean
     from .insert import insert_alloc
     from .temp import temp_alloc
     from .tetris_opt import tetris_opt
-    fused = insert_alloc(proc)
-    temp_alloc(proc, fused)
+    temp_alloc(proc, insert_alloc(proc))
     tetris_opt(proc)
     temp_clean(proc)
     return proc

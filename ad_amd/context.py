@@ -1,33 +1,39 @@
-"""IR containers and the global id counters.
+"""Tracing state and the procedural IR container.
 
-Restates autodiff/context.py:7-159.  ``Proc`` is the procedural IR the device
-backend consumes; ``Block`` records construction order while a program is
-traced; ``Context`` hands out ids.  Id allocation order decides node ids,
-fusion ids, toposort tie-breaking and therefore arena offsets, so every id is
-requested at the same point as in the reference.
+* ``Block`` -- the scope a program is traced into (the main program, or the
+  body of an ``ir_for``).  It keeps the nodes no later node has consumed,
+  in construction order: the sinks the compiler starts from.
+* ``Proc`` -- the procedural IR: an ordered command list (nodes, fused
+  groups, allocation commands, loops whose body is a ``Proc``) that a
+  device executes in order.
+* ``context`` -- the single global tracer: the open blocks and the id
+  sequences.  Node ids, fusion ids, Proc ids and program ids are handed out
+  at the same points as in the reference (autodiff/context.py:96-157), since
+  every later pass orders its work by them.
 """
-from typing import Callable, Dict, Optional, Tuple
+from typing import Callable, Dict, List
 
 
 def indent_str(obj, size: int = 1, s: str = "    ") -> str:
+    """``obj`` printed with every line indented ``size`` times by ``s``."""
     pad = s * size
     return "\n".join(pad + line for line in str(obj).splitlines())
 
 
 class Proc:
-    """Ordered command list: nodes, fused groups, alloc entries, loops."""
+    """An ordered command list with an id of its own."""
 
-    def __init__(self, proc):
+    def __init__(self, proc: List):
         self.procedure = proc
         self.id = context.get_proc_id()
 
     def __repr__(self):
-        out = ""
+        parts = []
         for cmd in self.procedure:
-            out += str(cmd) + "\n"
-            if hasattr(cmd, "proc"):
-                out += indent_str(str(cmd.get_proc())) + "\n"
-        return out
+            parts.append(f"{cmd}\n")
+            if hasattr(cmd, "proc"):               # a loop: its body, indented
+                parts.append(indent_str(cmd.get_proc()) + "\n")
+        return "".join(parts)
 
     def insert(self, idx, val):
         self.procedure.insert(idx, val)
@@ -36,77 +42,85 @@ class Proc:
         self.procedure.append(val)
 
     def walk(self, func: Callable, step_fused: bool = True, step_proc: bool = True):
-        """Apply ``func(cmd, proc_id)`` to every command; ``None`` deletes it.
-
-        Fused groups are entered when ``step_fused`` and loop bodies when
-        ``step_proc`` (context.py:29-47)."""
+        """Replace every command ``c`` by ``func(c, self.id)`` in place; a
+        ``None`` result deletes it.  With ``step_fused`` the members of a
+        fused group are visited instead of the group, with ``step_proc`` the
+        commands of a loop body (with that body's id) instead of the loop."""
         from .fusion.base import FuseBase
         from .node import Node
-        for idx in range(len(self.procedure)):
-            cmd = self.procedure[idx]
-            if isinstance(cmd, FuseBase) and step_fused:
-                cmd.nodes = [func(n, self.id) for n in cmd.nodes]
-                cmd.nodes = [n for n in cmd.nodes if n is not None]
-            elif isinstance(cmd, Node) and cmd.get_proc() is not None and step_proc:
+        for i, cmd in enumerate(self.procedure):
+            if step_fused and isinstance(cmd, FuseBase):
+                for j, member in enumerate(cmd.nodes):
+                    cmd.nodes[j] = func(member, self.id)
+                cmd.nodes = [m for m in cmd.nodes if m is not None]
+            elif step_proc and isinstance(cmd, Node) and cmd.get_proc() is not None:
                 cmd.proc.walk(func, step_fused, step_proc)
             else:
-                self.procedure[idx] = func(cmd, self.id)
+                self.procedure[i] = func(cmd, self.id)
         self.procedure = [c for c in self.procedure if c is not None]
 
 
 class Block:
-    """Nodes traced into one scope, keyed by id with their construction slot.
-
-    A node is dropped from its block when a later node consumes it, so the
-    block ends up holding the graph's sinks in construction order."""
+    """Traced scope.  While tracing, ``nodes`` maps id -> node for the nodes
+    not yet consumed, in construction order; ``convert_to_nodes`` freezes it
+    into that ordered list, which the compile passes then edit."""
 
     def __init__(self, id_override=None):
-        self.nodes: Dict[int, Tuple[object, int]] = dict()
-        self.position = 0
-        self.id = id_override if id_override is not None else context.get_block_id()
+        self.nodes: Dict[int, object] = {}
+        self.id = context.get_block_id() if id_override is None else id_override
 
     def add_to_dep(self, node):
-        self.nodes[node.id] = (node, self.position)
-        self.position += 1
+        self.nodes.pop(node.id, None)
+        self.nodes[node.id] = node
+
+    def remove_from_dep(self, other):
+        self.nodes.pop(other.id, None)
 
     def __len__(self):
         return len(self.nodes)
 
-    def remove_from_dep(self, other):
-        if other.id in self.nodes:
-            del self.nodes[other.id]
-
     def to_list(self):
-        if isinstance(self.nodes, list):
-            return self.nodes
-        ordered = sorted(self.nodes.values(), key=lambda kv: kv[1])
-        return [kv[0] for kv in ordered]
+        return self.nodes if isinstance(self.nodes, list) else list(self.nodes.values())
 
     def convert_to_nodes(self):
-        if isinstance(self.nodes, list):
-            return
         self.nodes = self.to_list()
 
     def __repr__(self):
-        return "\n".join(f"{i + 1}) {n!r}" for i, n in enumerate(self.nodes)) + "\n"
+        return "".join(f"{i}) {n!r}\n" for i, n in enumerate(self.nodes, start=1))
 
 
 class Context:
-    """Global tracing state (context.py:96-157)."""
+    """The global tracer: the stack of open blocks (``procedure[0]`` is the
+    main program) and the id sequences."""
 
     def __init__(self):
-        self.id = -1
-        self.proc_id = -1
-        self.block_id = 0
-        self.program_id = -1
-        self.grads_seen = dict()
-        self.connections = dict()
+        self._next = {"node": 0, "proc": 0, "block": 1, "program": 0}
+        self.grads_seen = {}          # state of the reverse pass (node.backward)
+        self.connections = {}
         self.conn_seen = set()
         self.procedure = [Block(0)]
-        self.lock_proc = False
+        self.lock_proc = False        # set once compilation starts: no more tracing
+
+    def _take(self, kind):
+        value = self._next[kind]
+        self._next[kind] = value + 1
+        return value
+
+    def get_id(self):
+        return self._take("node")
+
+    def get_proc_id(self):
+        return self._take("proc")
+
+    def get_block_id(self):
+        return self._take("block")
+
+    def get_prog_id(self):
+        return self._take("program")
 
     def reset(self):
-        """Start a fresh program (the reference relies on process isolation)."""
+        """Forget the traced program: fresh ids and an empty main block (the
+        reference gets this from running each program in its own process)."""
         self.__init__()
         from . import helper, linearize
         from .opt import simplify as opt_simplify
@@ -123,39 +137,25 @@ class Context:
             self.procedure[-1].remove_from_dep(other)
 
     def add_proc(self):
+        """Open the block of a loop body."""
         self.procedure.append(Block())
 
     def pop_proc(self):
-        assert len(self.procedure) > 1, "Attempt to pop main procedure!"
-        ret = self.procedure.pop(-1)
-        ret.convert_to_nodes()
-        return ret
+        """Close the innermost loop body and return its frozen block."""
+        assert len(self.procedure) > 1, "no loop body is open; the main block stays"
+        block = self.procedure.pop()
+        block.convert_to_nodes()
+        return block
 
     def prep_exec(self):
         self.lock_proc = True
         self.procedure[0].convert_to_nodes()
 
-    def get_id(self):
-        self.id += 1
-        return self.id
-
-    def get_proc_id(self):
-        self.proc_id += 1
-        return self.proc_id
-
-    def get_block_id(self):
-        self.block_id += 1
-        return self.block_id
-
-    def get_prog_id(self):
-        self.program_id += 1
-        return self.program_id
+    def main_proc(self):
+        return self.procedure[0]
 
     def __repr__(self):
         return repr(self.procedure[0])
-
-    def main_proc(self):
-        return self.procedure[0]
 
 
 context = Context()

@@ -1,8 +1,15 @@
-"""Greedy fusion accumulator (autodiff/fusion/base.py:16-89)."""
+"""A fused group under construction (the reference's FuseBase,
+autodiff/fusion/base.py:16-89).
+
+A group starts at a node its family accepts as a first member and grows by
+one node at a time: a candidate must read something the group already
+produces (unless the family fuses unconnected nodes), and it is placed
+right after the latest member it may follow.  The members run as one kernel
+of the family's template; the group prints as the reference's listings show
+it."""
 from enum import Enum
 from typing import List
 
-from ..context import indent_str
 from ..node import Node
 from .helper import get_deps, get_res
 
@@ -10,66 +17,68 @@ __all__ = ["FuseResult", "FuseBase"]
 
 
 class FuseResult(Enum):
-    INIT = 1
-    ADD = 2
-    NONE = 3
+    INIT = 1          # the node started the group
+    ADD = 2           # the node joined the group
+    NONE = 3          # the node stays out
+
+
+def _indented(text: str, pad: str = "    ") -> str:
+    return "\n".join(pad + line for line in text.splitlines())
 
 
 class FuseBase:
-    def __init__(self, dep_match=True, should_flatten=False):
+    """Families define ``can_start(node)`` and ``can_follow(member, node)``;
+    neither may use instance state (the fusion pass asks ``can_start`` of a
+    family before creating a group, which draws a fresh id)."""
+
+    def __init__(self, dep_match: bool = True, should_flatten: bool = False):
         from ..context import context
-        self.dep_match = dep_match
-        self.should_flatten = should_flatten
-        self.result_tracker = set()
+        self.dep_match = dep_match              # a joining node must read the group's results
+        self.should_flatten = should_flatten    # keep a foreign group whole when adding it
+        self.result_tracker = set()             # ids the members produce
         self.nodes: List[Node] = []
         self.init_node = None
         self.fuse_id = context.get_id()
 
-    def _add_node(self, add, index=None):
-        for r in get_res(add):
-            self.result_tracker.add(r)
-        if isinstance(index, int):
-            self.nodes.insert(index, add)
+    def can_start(self, node) -> bool:
+        raise NotImplementedError(f"{type(self).__name__} declares no first member")
+
+    def can_follow(self, member, node) -> bool:
+        raise NotImplementedError(f"{type(self).__name__} declares no successor rule")
+
+    def _place(self, item, at=None):
+        self.result_tracker.update(get_res(item))
+        if at is None:
+            self.nodes.append(item)
         else:
-            self.nodes.append(add)
+            self.nodes.insert(at, item)
 
-    def add(self, n, index=None):
-        if isinstance(n, FuseBase):
-            if self.should_flatten and type(self) != type(n):
-                self._add_node(n, index)
-            else:
-                for node in n.nodes:
-                    self._add_node(node, index)
-        elif isinstance(n, Node):
-            self._add_node(n, index)
+    def add(self, item, index=None):
+        """Add a node, or the members of another group (the group whole when
+        ``should_flatten`` and it is of another family)."""
+        if isinstance(item, FuseBase) and not (self.should_flatten and type(item) is not type(self)):
+            for member in item.nodes:
+                self._place(member, index)
+        elif isinstance(item, (Node, FuseBase)):
+            self._place(item, index)
         else:
-            raise TypeError(f"Invalid type: {type(n)}")
-
-    def _fuse(self, node_one, node_two):
-        raise NotImplementedError
-
-    def _init(self, node):
-        raise NotImplementedError
+            raise TypeError(f"a fused group holds nodes, not {type(item).__name__}")
 
     def attempt_fuse(self, node, deps=None) -> FuseResult:
-        """Start the group with ``node``, or append it right after the last
-        member it can follow (fusion/base.py:59-77)."""
-        if len(self.nodes) == 0 and self._init(node):
+        if not self.nodes and self.can_start(node):
             self.init_node = node
             self.add(node)
             return FuseResult.INIT
-        if deps is None:
-            deps = get_deps(node)
-        if self.dep_match and len(self.result_tracker.intersection(deps)) == 0:
+        reads = get_deps(node) if deps is None else deps
+        if self.dep_match and not (self.result_tracker & reads):
             return FuseResult.NONE
-        for idx, n in enumerate(reversed(self.nodes)):
-            if self._fuse(n, node):
-                self.add(node, len(self.nodes) - idx)
+        for back, member in enumerate(reversed(self.nodes)):
+            if self.can_follow(member, node):
+                self.add(node, len(self.nodes) - back)
                 return FuseResult.ADD
         return FuseResult.NONE
 
     def __repr__(self):
-        out = f"{type(self).__name__} Fusion (fuse_id: {self.fuse_id}):\n"
-        for n in self.nodes:
-            out += indent_str(str(n)) + "\n"
-        return out[:-1]
+        lines = [f"{type(self).__name__} Fusion (fuse_id: {self.fuse_id}):"]
+        lines += [_indented(str(n)) for n in self.nodes]
+        return "\n".join(lines)

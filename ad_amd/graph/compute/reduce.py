@@ -1,6 +1,6 @@
-"""Row reduction over the last axis of a 2-D operand
-(autodiff/graph/compute/reduce.py:6-43)."""
-from copy import deepcopy
+"""SUM or MAX over the last axis of a 2-D operand, [V, R] -> [V]
+(autodiff/graph/compute/reduce.py).  Other axes and ranks reach it through
+``Node.sum`` / ``Node.max``, which permute and view around it."""
 from enum import Enum
 
 from ...node import Node
@@ -17,24 +17,14 @@ class ReduceNode(Node):
     __match_args__ = ("child", "op")
 
     def __init__(self, child: Node, op: ReduceOp):
-        assert len(child.shape) == 2, "Reduce shape must be 2-dim"
-        res_shape = deepcopy(child.shape)
-        del res_shape[-1]
-        super().__init__([child], res_shape)
+        if len(child.shape) != 2:
+            raise AssertionError(f"a reduction takes a 2-D operand, got {child.shape}")
+        super().__init__([child], child.shape[:-1])
         self.op = op
 
-    def _bck(self, grad: Node):
-        repeat_n = self.children_shapes[0][-1]
-        return grad.unsqueeze(-1).broadcast(-1, repeat_n)
-
-    def __repr__(self):
-        sh = self.children_shapes[0]
-        size_str = f"(Vec/X: {sh[0]}, Reduce/Y: {sh[1]})"
-        if self.kargs[0].is_none() or self.kres.is_none():
-            return f"{self.id} = {self.op.name} on dim: -1 {size_str} --> ({self.child.id})"
-        return f"{self.kres} = {self.op.name} on dim: -1 {size_str} --> ({self.kargs[0]})"
+    def _label(self):
+        rows, length = self.children_shapes[0]
+        return f"{self.op.name} on dim: -1 (Vec/X: {rows}, Reduce/Y: {length})"
 
     def repeat_helper(self, is_child):
-        if is_child:
-            return (self.id,)
-        return ("Reduce", self.op.value)
+        return (self.id,) if is_child else ("Reduce", self.op.value)

@@ -1,5 +1,5 @@
-"""Materialise a strided view as a dense buffer
-(autodiff/graph/data/contigious.py:7-25)."""
+"""Materialise a view chain (permute, view, broadcast, index, concat) as a
+dense buffer (autodiff/graph/data/contigious.py)."""
 from ...node import Node
 
 __all__ = ["ContigiousNode"]
@@ -11,15 +11,10 @@ class ContigiousNode(Node):
     def __init__(self, child: Node):
         super().__init__([child], child.shape)
 
-    def _bck(self, grad: Node):
-        return grad
-
     def __repr__(self):
-        if self.kargs[0].is_none() or self.kres.is_none():
-            return f"{self.id} = Contigious ({self.child.id})"
-        return f"{self.kres} = Contigious ({self.child.id}: {self.kargs[0]})"
+        if self._lowered():
+            return f"{self.kres} = Contigious ({self.child.id}: {self.kargs[0]})"
+        return f"{self.id} = Contigious ({self.child.id})"
 
     def repeat_helper(self, is_child):
-        if is_child:
-            return (self.id,)
-        return ("Contigious",)
+        return (self.id,) if is_child else ("Contigious",)

@@ -1,4 +1,7 @@
-"""Leaf tensor holding host data (autodiff/graph/tensor.py:11-64)."""
+"""Leaf value with host data (autodiff/graph/tensor.py).  Its buffer is
+initialised from ``arr`` (float32) and, after execution, ``arr`` holds the
+device's final values.  ``grad()`` is the node of its accumulated gradient
+once a loss has been differentiated."""
 import numpy as np
 
 from ..node import Node
@@ -13,43 +16,33 @@ class Tensor(Node):
         self.grad_tensor = None
         self.requires_grad = requires_grad
 
-    def _bck(self, grad):
-        if not isinstance(grad, Node):
-            raise TypeError("Backward on tensor grad is not tensoor")
-        if self.requires_grad:
-            if self.grad_tensor is None:
-                self.grad_tensor = grad
-            else:
-                self.grad_tensor += grad     # an in-place ADD node
-        return None
-
     def grad(self):
         if self.grad_tensor is None:
-            raise RuntimeError(f"Gradient on tensor {self.id} is none! Make sure you call .backward()")
+            raise RuntimeError(f"tensor {self.id} has no gradient: call .backward() on a loss that uses it")
         return self.grad_tensor
-
-    def repeat_helper(self, is_child):
-        return ("Tensor", self.id)
 
     def __repr__(self) -> str:
         return f"Tensor(id: {self.id}, orig_shape: {self.shape})"
 
-    @staticmethod
-    def from_torch(arr, requires_grad: bool = False):
-        return Tensor(arr.numpy(), requires_grad=requires_grad)
+    def repeat_helper(self, is_child):
+        return ("Tensor", self.id)
 
-    @staticmethod
-    def randn(shape, requires_grad=False):
-        return Tensor(np.random.randn(*shape), requires_grad)
+    @classmethod
+    def from_torch(cls, arr, requires_grad: bool = False):
+        return cls(arr.numpy(), requires_grad=requires_grad)
 
-    @staticmethod
-    def fill(val: float, shape, requires_grad=False):
-        return Tensor(np.full(tuple(shape), val), requires_grad)
+    @classmethod
+    def randn(cls, shape, requires_grad=False):
+        return cls(np.random.randn(*shape), requires_grad)
 
-    @staticmethod
-    def ones(shape, requires_grad=False):
-        return Tensor.fill(1.0, shape, requires_grad)
+    @classmethod
+    def fill(cls, val: float, shape, requires_grad=False):
+        return cls(np.full(tuple(shape), val), requires_grad)
 
-    @staticmethod
-    def zeros(shape, requires_grad=False):
-        return Tensor.fill(0.0, shape, requires_grad)
+    @classmethod
+    def ones(cls, shape, requires_grad=False):
+        return cls.fill(1.0, shape, requires_grad)
+
+    @classmethod
+    def zeros(cls, shape, requires_grad=False):
+        return cls.fill(0.0, shape, requires_grad)

@@ -186,7 +186,7 @@ def fuse(g_dep_id) -> Proc:
     init_taken = set()
 
     for family in _FUSION_FAMILIES:
-        probe = family.__new__(family)       # only for _init(); allocates no id
+        probe = family.__new__(family)       # only for can_start(); allocates no id
         first_layer = 0
         while True:
             op_entry = family()
@@ -194,7 +194,7 @@ def fuse(g_dep_id) -> Proc:
             did_start = False
             # skip leading layers in which no untaken node can start a group
             while first_layer < len(toposort_res) and not any(
-                    nid not in init_taken and probe._init(id_to_node[nid])
+                    nid not in init_taken and probe.can_start(id_to_node[nid])
                     for nid in toposort_res[first_layer]):
                 first_layer += 1
             for layer_idx in range(first_layer, len(toposort_res)):
