@@ -4,8 +4,10 @@
 The output command order is the order of the second toposort's layers, and
 every container whose iteration order feeds it (dicts keyed in traversal
 order, sets of ids) is built with the same sequence of operations as the
-reference.  Two things differ from a literal reading, neither of which can
-change the result:
+reference.  The dependency walk runs on an explicit stack (no recursion
+depth limit), visiting nodes in the order a depth-first recursion does.
+Things that differ from a literal reading, none of which can change the
+result:
 
 * a command's dependency set is computed once per ``fuse`` call and reused
   (kernel args are not renamed while fusing);
@@ -18,7 +20,6 @@ change the result:
   layer at each block (``_EagerWhiteList``, the reference's way, kept as the
   check); both give the same set at every point of the scan.
 """
-from copy import deepcopy
 from typing import Dict, List
 
 from .context import Block, Proc
@@ -29,78 +30,91 @@ from .helper import walk_graph
 from .node import Node
 from .toposort import toposort
 
-global_deps: Dict[int, Dict[int, set]] = {}
+global_deps: Dict[int, Dict[int, set]] = {}      # block id -> node id -> ids it waits for
 id_to_node: Dict[int, object] = {}
-block_to_node: Dict[int, int] = {}
-alr_defined_global: Dict[int, list] = {}
+block_to_node: Dict[int, int] = {}               # loop body block id -> loop node id
 
 
 def reset_state():
-    global global_deps, id_to_node, block_to_node, alr_defined_global
+    global global_deps, id_to_node, block_to_node
     global_deps = {}
     id_to_node = {}
     block_to_node = {}
-    alr_defined_global = {}
 
 
-def insert_to_global_dep(block_id: int, key: int, value):
-    if block_id not in global_deps:
-        global_deps[block_id] = dict()
-    if key not in global_deps[block_id]:
-        global_deps[block_id][key] = set({value}) if value is not None else set({})
-    elif value is not None:
-        global_deps[block_id][key].add(value)
+def _wait_for(block_id: int, node_id: int, dep):
+    """Record that ``node_id`` (in block ``block_id``) waits for ``dep``;
+    ``dep`` None records the node with nothing to wait for yet."""
+    waits = global_deps.setdefault(block_id, {}).setdefault(node_id, set())
+    if dep is not None:
+        waits.add(dep)
 
 
-def get_deps_global(block: Block, alr_defined: Dict[int, int] = None):
-    """Record, per block, ``node -> ids it waits on``.  Reads of ids defined
-    in an enclosing block become a dependency of the enclosing loop node
-    (linearize.py:31-101)."""
-    if alr_defined is None:
-        alr_defined = dict()
-    if block.id not in alr_defined_global:
-        alr_defined_global[block.id] = list(alr_defined.keys())
+def get_deps_global(block: Block, outer: Dict[int, int] = None):
+    """Fill ``global_deps[block.id]``: for every node traced in ``block``,
+    the ids it must wait for (linearize.py:31-101).
 
-    defined = dict()
-    vars_need_dep = dict()
-    for n in block.nodes:
-        inner_bl = n.get_block()
-        if inner_bl:
-            def_block, need_dep_block = get_deps_global(inner_bl, alr_defined | defined)
-            for (dep, block_id) in deepcopy(list(need_dep_block.items())):
-                if block_id == block.id:
-                    insert_to_global_dep(block.id, n.id, dep)
-                    del need_dep_block[dep]
-            defined.update(def_block)
-            vars_need_dep.update(need_dep_block)
-            block_to_node[inner_bl.id] = n.id
-        else:
-            _collect(n, set(), block, alr_defined, defined, vars_need_dep)
-    return defined, vars_need_dep
+    ``outer`` maps ids defined in enclosing blocks to their block.  A read of
+    such an id is not an edge inside this block: it is returned in
+    ``needs`` (id -> defining block), and the enclosing block whose loop
+    contains this one records it as a wait of that loop node.  A read of an
+    id defined in a sibling loop body waits for that loop node.  Returns
+    ``(defined, needs)``: ids defined in this block (and its loops), and
+    outer ids it reads."""
+    outer = {} if outer is None else outer
+    defined: Dict[int, int] = {}
+    needs: Dict[int, int] = {}
+    for node in block.nodes:
+        body = node.get_block()
+        if body is None:
+            _collect(node, block, outer, defined, needs)
+            continue
+        body_defined, body_needs = get_deps_global(body, outer | defined)
+        for dep, where in list(body_needs.items()):
+            if where == block.id:
+                _wait_for(block.id, node.id, dep)
+                del body_needs[dep]
+        defined.update(body_defined)
+        needs.update(body_needs)
+        block_to_node[body.id] = node.id
+    return defined, needs
 
 
-def _collect(n, visited, block, alr_defined, defined, vars_need_dep):
-    if n.id in visited or n.id in alr_defined:
+def _collect(root, block, outer, defined, needs):
+    """Depth-first from ``root`` through the ids each node reads, recording
+    waits.  A node's reads are visited in order, each one's subtree before
+    the next read; a node is marked defined after its reads (post-order).
+    Nodes of outer blocks, or already entered from this root, are not
+    entered again; ids defined in another loop body stand for that loop."""
+    entered = set()
+
+    def enterable(node):
+        return isinstance(node, Node) and node.id not in entered and node.id not in outer
+
+    if not enterable(root):
         return
-    if isinstance(n, Node):
-        for dep in n.kargs_child_ids():
-            should_visit = True
-            value = dep
-            if dep in alr_defined:
-                value = None
-                should_visit = False
-                vars_need_dep[dep] = alr_defined[dep]
-            if dep in defined:
-                block_id_defined = defined[dep]
-                if block_id_defined != block.id:
-                    should_visit = False
-                    value = block_to_node[block_id_defined]
-            insert_to_global_dep(block.id, n.id, value)
-            if should_visit:
-                visited.add(n.id)
-                _collect(id_to_node[dep], visited, block, alr_defined, defined, vars_need_dep)
-        if n.id not in defined:
-            defined[n.id] = block.id
+    stack = [(root, root.kargs_child_ids(), [0])]
+    while stack:
+        node, reads, cursor = stack[-1]
+        if cursor[0] == len(reads):
+            stack.pop()
+            if node.id not in defined:
+                defined[node.id] = block.id
+            continue
+        dep = reads[cursor[0]]
+        cursor[0] += 1
+        target, descend = dep, True
+        if dep in outer:
+            target, descend = None, False
+            needs[dep] = outer[dep]
+        if dep in defined and defined[dep] != block.id:
+            target, descend = block_to_node[defined[dep]], False
+        _wait_for(block.id, node.id, target)
+        if descend:
+            entered.add(node.id)
+            child = id_to_node[dep]
+            if enterable(child):
+                stack.append((child, child.kargs_child_ids(), [0]))
 
 
 _FUSION_FAMILIES = [DPElwFuse, ReduceElwFuse, ElwFuse]
@@ -272,7 +286,7 @@ def fuse(g_dep_id) -> Proc:
 
 
 def linearize(main_block: Block) -> Proc:
-    global global_deps, id_to_node, block_to_node, alr_defined_global
+    global global_deps, id_to_node, block_to_node
     id_to_node = {}
 
     def insert_id_to_node(node, _):
@@ -283,7 +297,6 @@ def linearize(main_block: Block) -> Proc:
 
     global_deps = {}
     block_to_node = {}
-    alr_defined_global = {}
-    _, d = get_deps_global(main_block)
-    assert len(d) == 0, "vars need dep not None!"
+    _, unresolved = get_deps_global(main_block)
+    assert not unresolved, f"reads of ids defined outside the program: {sorted(unresolved)}"
     return fuse(0)
