@@ -616,6 +616,79 @@ int adhip_graph_end(adhip_ctx* ctx, adhip_graph** out) {
   return 0;
 }
 
+int adhip_graph_end_dag(adhip_ctx* ctx, int32_t n_nodes, const int32_t* dep_offsets, const int32_t* deps,
+                        adhip_graph** out) {
+  if (!ctx || !out || n_nodes < 0 || (n_nodes && !dep_offsets)) return fail(ctx, ADHIP_E_ARG, "bad argument");
+  if (!ctx->capturing) return fail(ctx, ADHIP_E_STATE, "not capturing");
+  ctx->capturing = false;
+  hipGraph_t graph = nullptr;
+  HIP_TRY(ctx, hipStreamEndCapture(ctx->stream, &graph));
+  auto drop = [&](int code, const char* fmt, auto... a) {
+    hipGraphDestroy(graph);
+    return fail(ctx, code, fmt, a...);
+  };
+  // the captured work is a chain: walk it from its root in capture order
+  std::vector<hipGraphNode_t> order;
+  size_t nroots = 0;
+  hipError_t e = hipGraphGetRootNodes(graph, nullptr, &nroots);
+  if (e != hipSuccess) return drop((int)e, "hipGraphGetRootNodes: %s", hipGetErrorString(e));
+  if (nroots > 1) return drop(ADHIP_E_STATE, "captured graph has %zu roots, expected a chain", nroots);
+  if (nroots == 1) {
+    hipGraphNode_t cur = nullptr;
+    e = hipGraphGetRootNodes(graph, &cur, &nroots);
+    if (e != hipSuccess) return drop((int)e, "hipGraphGetRootNodes: %s", hipGetErrorString(e));
+    while (true) {
+      order.push_back(cur);
+      size_t nnext = 0;
+      e = hipGraphNodeGetDependentNodes(cur, nullptr, &nnext);
+      if (e != hipSuccess) return drop((int)e, "hipGraphNodeGetDependentNodes: %s", hipGetErrorString(e));
+      if (nnext == 0) break;
+      if (nnext > 1) return drop(ADHIP_E_STATE, "captured node %zu has %zu successors, expected a chain",
+                                 order.size() - 1, nnext);
+      hipGraphNode_t next = nullptr;
+      e = hipGraphNodeGetDependentNodes(cur, &next, &nnext);
+      if (e != hipSuccess) return drop((int)e, "hipGraphNodeGetDependentNodes: %s", hipGetErrorString(e));
+      cur = next;
+    }
+  }
+  if ((int64_t)order.size() != n_nodes)
+    return drop(ADHIP_E_ARG, "captured %zu graph nodes, the dependency lists describe %d", order.size(), n_nodes);
+  // replace the chain edges by the given dependencies
+  std::vector<hipGraphNode_t> from, to;
+  for (size_t i = 1; i < order.size(); ++i) {
+    from.push_back(order[i - 1]);
+    to.push_back(order[i]);
+  }
+  if (!from.empty()) {
+    e = hipGraphRemoveDependencies(graph, from.data(), to.data(), from.size());
+    if (e != hipSuccess) return drop((int)e, "hipGraphRemoveDependencies: %s", hipGetErrorString(e));
+  }
+  from.clear();
+  to.clear();
+  for (int32_t i = 0; i < n_nodes; ++i) {
+    for (int32_t k = dep_offsets[i]; k < dep_offsets[i + 1]; ++k) {
+      const int32_t d = deps[k];
+      if (d < 0 || d >= i) return drop(ADHIP_E_ARG, "node %d depends on node %d (must be an earlier node)", i, d);
+      from.push_back(order[d]);
+      to.push_back(order[i]);
+    }
+  }
+  if (!from.empty()) {
+    e = hipGraphAddDependencies(graph, from.data(), to.data(), from.size());
+    if (e != hipSuccess) return drop((int)e, "hipGraphAddDependencies: %s", hipGetErrorString(e));
+  }
+  auto* g = new adhip_graph();
+  g->graph = graph;
+  e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    hipGraphDestroy(g->graph);
+    delete g;
+    return fail(ctx, (int)e, "hipGraphInstantiate: %s", hipGetErrorString(e));
+  }
+  *out = g;
+  return 0;
+}
+
 int adhip_graph_launch(adhip_ctx* ctx, adhip_graph* g) {
   if (!ctx || !g) return fail(ctx, ADHIP_E_ARG, "null argument");
   HIP_TRY(ctx, hipGraphLaunch(g->exec, ctx->stream));

@@ -71,6 +71,19 @@ class _Launch:
         self.cmd, self.plan, self.args, self.reads, self.writes = cmd, plan, args, reads, writes
 
 
+def _transitive_reduction(deps):
+    """The same order with the fewest edges: an edge j -> i is dropped when
+    another dependency of i already follows j."""
+    before, out = [], []
+    for d in deps:
+        reach = 0
+        for j in d:
+            reach |= before[j] | (1 << j)
+        before.append(reach)
+        out.append([j for j in d if not any(before[k] >> j & 1 for k in d if k != j)])
+    return out
+
+
 class HIPDevice(Device):
     """The reference's device protocol on one MI355X (see the module notes).
 
@@ -110,6 +123,14 @@ class HIPDevice(Device):
       storage of its own, so reuse of memory between variables orders no
       launches; costs the sum of the variables' sizes instead of the packed
       high-water mark);
+    * ``graph_dag`` -- a captured loop body keeps only the dependencies the
+      schedule found (launches touching overlapping memory, one writing, in
+      Proc order; transitively reduced), so independent launches may run at
+      the same time; off (the default), the graph is the captured chain.
+      Measured on C5 (647 launches, critical path 11.3 of 16.8 ms of kernel
+      time, at most 10 launches side by side): 16.74 against 16.68 ms per
+      step, C4 1.631 against 1.620 ms -- the runtime gains nothing from the
+      parallel branches;
     * ``stream_min_bytes`` -- float4 reads of a range of at least this many
       bytes that no other command reads (and no loop iteration reads again),
       and writes of such a range no command reads, bypass the caches
@@ -121,8 +142,10 @@ class HIPDevice(Device):
                  group_launches: bool = True, lanes: int = 1, receiver_lag: int = 0,
                  exact_reduce: bool = False, feeder_offset_zero: bool = False,
                  strict_temps: bool = False, dot_precision: str = "fp32", bf16_min_macs: int = 1 << 30,
-                 loop_unroll: int = 32, arena: str = "packed", stream_min_bytes: int = 32 << 20):
+                 loop_unroll: int = 32, arena: str = "packed", stream_min_bytes: int = 32 << 20,
+                 graph_dag: bool = False):
         super().__init__()
+        self.graph_dag = graph_dag
         assert arena in ("packed", "unpacked"), "arena must be packed or unpacked"
         assert not (arena == "unpacked" and feeder_offset_zero), \
             "feeder_offset_zero writes into the packed arena; it needs arena='packed'"
@@ -172,6 +195,7 @@ class HIPDevice(Device):
         self._parity = 0
         self._slot = 0
         self._schedules = {}         # Proc id -> one-lane items (captured into graphs)
+        self.stretch_graphs = {}     # Proc id -> per stretch: [(kernel, instances, deps)] per launch group
         self._lane_schedules = {}    # Proc id -> items over self.lanes lanes (uncaptured runs)
         self._capturing = False
         self.stats = {"kernels": 0, "unique_sources": 0, "multipass_cmds": 0, "launches_per_iter": 0}
@@ -412,12 +436,14 @@ class HIPDevice(Device):
                 if item[0] in ("cmd", "record", "wait"):
                     out.append(item)
                     continue
-                _, plan, row, count, lane = item
+                _, plan, row, count, lane, g, deps = item
                 if row not in launchers:
                     grid = (plan.grid[0], plan.grid[1], count)
                     launchers[row] = self.ctx.launcher_on(funcs[plan.name], grid, plan.block,
                                                           plan.shared, [tbase + row])
-                out.append(("launch", launchers[row], lane))
+                # (kind, launcher, lane, index in its stretch, groups of the
+                # stretch it follows, whether the launch makes a graph node)
+                out.append(("launch", launchers[row], lane, g, deps, min(plan.grid[:2]) > 0 and count > 0))
             return out
         for pid_proc, (items, lane_items) in sched.items():
             self._schedules[pid_proc] = bind(items)
@@ -496,8 +522,15 @@ class HIPDevice(Device):
                     members = [launches[i] for i in group]
                     plans_of.append((members[0].plan, len(members)))
                     rows.append(add_rows([self._arg_values(m.plan, m.cmd.program_id) for m in members]))
+                # the launch groups of this stretch and the earlier groups each
+                # must follow (kernel name, instances, dependencies)
+                self.stretch_graphs.setdefault(p.id, []).append(
+                    [(plans_of[g][0].name, plans_of[g][1], deps[g],
+                      [r for i in groups[g] for r in launches[i].reads],
+                      [w for i in groups[g] for w in launches[i].writes]) for g in range(len(groups))])
                 # one lane: the groups in order (the form captured into graphs)
-                one = [("launch", plans_of[g][0], rows[g], plans_of[g][1], 0) for g in range(len(groups))]
+                one = [("launch", plans_of[g][0], rows[g], plans_of[g][1], 0, g, tuple(deps[g]))
+                       for g in range(len(groups))]
                 items.extend(one)
                 if self.lanes == 1:
                     lane_items.extend(one)
@@ -516,7 +549,8 @@ class HIPDevice(Device):
                 for g in range(len(groups)):
                     for d in waits[g]:
                         lane_items.append(("wait", lane_of[g], recorded[d]))
-                    lane_items.append(("launch", plans_of[g][0], rows[g], plans_of[g][1], lane_of[g]))
+                    lane_items.append(("launch", plans_of[g][0], rows[g], plans_of[g][1], lane_of[g], g,
+                                       tuple(deps[g])))
                     if g in needed:
                         recorded[g] = self._new_event()
                         lane_items.append(("record", lane_of[g], recorded[g]))
@@ -697,7 +731,9 @@ class HIPDevice(Device):
     def _capture(self, inner, unroll, count):
         """Graphs of ``count`` consecutive iterations of a loop body, one per
         staging parity (one only when the body has no Feeder or Receiver);
-        iteration u of parity p reads Feeder slot ``p * unroll + u``."""
+        iteration u of parity p reads Feeder slot ``p * unroll + u``.  With
+        ``graph_dag`` the captured chain is rewired to the schedule's
+        dependencies (``_dag_deps``)."""
         graphs = []
         for parity in (0, 1):
             self._capturing, self._parity = True, parity
@@ -708,12 +744,66 @@ class HIPDevice(Device):
                 for u in range(count):
                     self._slot = parity * unroll + u
                     self._run_scheduled(inner)
-            finally:
+            except BaseException:
                 self._capturing = False
+                self.ctx.graph_end()          # close the capture; the error propagates
+                raise
+            self._capturing = False
+            if self.graph_dag:
+                graphs.append(self.ctx.graph_end_dag(self._dag_deps(inner, count)))
+            else:
                 graphs.append(self.ctx.graph_end())
             if not self._graph_feeders and not self._graph_receivers:
                 break                    # one graph serves every launch
         return graphs
+
+    def _dag_deps(self, inner, count):
+        """For the nodes a capture of ``count`` iterations of ``inner`` made,
+        in capture order: the earlier nodes each must follow.  A launch
+        follows the launches of its stretch the schedule says it depends on
+        (every pair touching overlapping memory, one writing, stays
+        ordered); a launch with none follows everything before its stretch.
+        A copy (a Feeder's staging slot, a Receiver's snapshot) follows
+        everything before it, and everything after it follows the copy."""
+        deps, frontier = [], []
+        stretch_base, stretch_nodes = None, []
+
+        def close_stretch():
+            nonlocal frontier, stretch_base, stretch_nodes
+            if stretch_base is None:
+                return
+            if stretch_nodes:
+                used = {d for n in stretch_nodes for d in deps[n] if d >= stretch_base}
+                frontier = [n for n in stretch_nodes if n not in used]
+            stretch_base, stretch_nodes = None, []
+
+        node_of = {}
+        for _ in range(count):
+            for item in self._schedules[inner.id]:
+                if item[0] == "launch":
+                    _, _, _, g, gdeps, makes_node = item
+                    if g == 0:
+                        close_stretch()
+                        stretch_base, node_of = len(deps), {}
+                    if not makes_node:
+                        node_of[g] = None
+                        continue
+                    mine = sorted({node_of[d] for d in gdeps if node_of.get(d) is not None})
+                    node_of[g] = len(deps)
+                    deps.append(mine if mine else list(frontier))
+                    stretch_nodes.append(node_of[g])
+                    continue
+                close_stretch()
+                cmd = item[1]
+                if isinstance(cmd, Receiver):
+                    copies = sum(1 for shape in cmd.shapes if prod(shape) > 0)
+                else:
+                    copies = 1 if isinstance(cmd, Feeder) and prod(cmd.shape) > 0 else 0
+                for _ in range(copies):
+                    deps.append(list(frontier))
+                    frontier = [len(deps) - 1]
+            close_stretch()
+        return _transitive_reduction(deps)
 
     def _fetch_receiver(self, r, parity):
         src = self._recv_slots[r.id][0][parity]

@@ -23,7 +23,7 @@ EXPORTS = [
     "adhip_module_function", "adhip_launch", "adhip_graph_begin", "adhip_graph_end",
     "adhip_graph_launch", "adhip_graph_destroy", "adhip_sync", "adhip_event_record",
     "adhip_event_elapsed", "adhip_lanes_reserve", "adhip_launch_on", "adhip_record_on", "adhip_wait_on",
-    "adhip_reduce_cols", "adhip_reduce_cols_noalloc",
+    "adhip_reduce_cols", "adhip_reduce_cols_noalloc", "adhip_graph_end_dag",
 ]
 
 
@@ -68,6 +68,7 @@ def load_library(path=LIB_PATH):
             "adhip_graph_begin": (i32, [vp]),
             "adhip_graph_end": (i32, [vp, c.POINTER(vp)]),
             "adhip_graph_launch": (i32, [vp, vp]),
+            "adhip_graph_end_dag": (i32, [vp, i32, c.POINTER(i32), c.POINTER(i32), c.POINTER(vp)]),
             "adhip_graph_destroy": (None, [vp]),
             "adhip_sync": (i32, [vp]),
             "adhip_event_record": (i32, [vp, i32]),
@@ -246,6 +247,20 @@ class Context:
     def graph_end(self):
         g = ctypes.c_void_p()
         self.check(self.lib.adhip_graph_end(self.h, ctypes.byref(g)), "adhip_graph_end")
+        return g
+
+    def graph_end_dag(self, deps):
+        """End the capture; ``deps[i]`` lists the earlier captured nodes node
+        ``i`` must follow (the chain's own edges are dropped)."""
+        offs = [0]
+        flat = []
+        for d in deps:
+            flat.extend(int(x) for x in d)
+            offs.append(len(flat))
+        o = (ctypes.c_int32 * len(offs))(*offs)
+        f = (ctypes.c_int32 * max(1, len(flat)))(*flat)
+        g = ctypes.c_void_p()
+        self.check(self.lib.adhip_graph_end_dag(self.h, len(deps), o, f, ctypes.byref(g)), "adhip_graph_end_dag")
         return g
 
     def graph_launch(self, g):

@@ -134,6 +134,16 @@ int  adhip_wait_on(adhip_ctx* ctx, int stream, int event);
  * every command from Python (device.py:121-129). */
 int  adhip_graph_begin(adhip_ctx* ctx);
 int  adhip_graph_end(adhip_ctx* ctx, adhip_graph** out);
+/* End a capture whose work formed a chain of n_nodes graph nodes (kernel
+ * launches and copies, in capture order) and replace the chain's edges by
+ * the given dependencies before instantiating: node i follows the nodes
+ * deps[dep_offsets[i] .. dep_offsets[i+1]) (earlier nodes only), so
+ * independent launches of a loop body may run concurrently on replay.  The
+ * reference replays a loop body command by command on one in-order queue
+ * (device.py:114-124); the dependencies given must order every pair of
+ * nodes touching overlapping memory, one of them writing. */
+int  adhip_graph_end_dag(adhip_ctx* ctx, int32_t n_nodes, const int32_t* dep_offsets, const int32_t* deps,
+                         adhip_graph** out);
 int  adhip_graph_launch(adhip_ctx* ctx, adhip_graph* g);
 void adhip_graph_destroy(adhip_graph* g);
 

@@ -123,6 +123,20 @@ class RecordingContext:
         self._capture = None
         return g
 
+    def graph_end_dag(self, deps):
+        """As ``graph_end``; the dependency lists are checked against the
+        captured nodes (one per launch with a non-empty grid, one per copy)
+        and kept in ``dags``."""
+        captured = [op for op in self._capture
+                    if op[0] == "copy" and op[3] > 0 or op[0] == "launch" and min(op[2]) > 0]
+        if len(deps) != len(captured):
+            self.errors.append(("dependency lists do not match the capture", len(deps), len(captured), 0))
+        for i, d in enumerate(deps):
+            if any(not 0 <= j < i for j in d):
+                self.errors.append(("dependency on a later node", i, list(d), 0))
+        self.dags = getattr(self, "dags", []) + [[list(d) for d in deps]]
+        return self.graph_end()
+
     def graph_launch(self, g):
         self.launches.extend(self._graphs[g])
 

@@ -56,6 +56,10 @@ class GraphRecordingContext:
         self.log.append(("graph_end", self._next))
         return self._next
 
+    def graph_end_dag(self, deps):
+        self.last_dag = [list(d) for d in deps]
+        return self.graph_end()
+
     def graph_launch(self, g):
         assert g in self.live_graphs, f"launch of destroyed graph {g}"
         self.log.append(("graph_launch", g))
