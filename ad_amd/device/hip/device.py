@@ -195,7 +195,7 @@ class HIPDevice(Device):
         self._parity = 0
         self._slot = 0
         self._schedules = {}         # Proc id -> one-lane items (captured into graphs)
-        self.stretch_graphs = {}     # Proc id -> per stretch: [(kernel, instances, deps)] per launch group
+        self.stretch_graphs = {}     # Proc id -> per stretch, per launch group: (kernel, instances, deps, reads, writes, flops)
         self._lane_schedules = {}    # Proc id -> items over self.lanes lanes (uncaptured runs)
         self._capturing = False
         self.stats = {"kernels": 0, "unique_sources": 0, "multipass_cmds": 0, "launches_per_iter": 0}
@@ -527,7 +527,8 @@ class HIPDevice(Device):
                 self.stretch_graphs.setdefault(p.id, []).append(
                     [(plans_of[g][0].name, plans_of[g][1], deps[g],
                       [r for i in groups[g] for r in launches[i].reads],
-                      [w for i in groups[g] for w in launches[i].writes]) for g in range(len(groups))])
+                      [w for i in groups[g] for w in launches[i].writes],
+                      sum(launches[i].plan.flops for i in groups[g])) for g in range(len(groups))])
                 # one lane: the groups in order (the form captured into graphs)
                 one = [("launch", plans_of[g][0], rows[g], plans_of[g][1], 0, g, tuple(deps[g]))
                        for g in range(len(groups))]

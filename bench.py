@@ -437,6 +437,64 @@ def published_config():
     return out
 
 
+def _merged_floats(ranges):
+    """Floats covered by a list of (buffer, lo, hi) ranges, overlaps once."""
+    by = {}
+    for buf, lo, hi in ranges:
+        by.setdefault(repr(buf), []).append((lo, hi))
+    total = 0
+    for segs in by.values():
+        segs.sort()
+        lo0, hi0 = segs[0]
+        for lo, hi in segs[1:]:
+            if lo > hi0:
+                total += hi0 - lo0
+                lo0, hi0 = lo, hi
+            else:
+                hi0 = max(hi0, hi)
+        total += hi0 - lo0
+    return total
+
+
+def probe(config, iters, out_path):
+    """Replay ``iters`` iterations of a configuration's loop body launch by
+    launch (no graph: kernel tracers and counter passes see every dispatch)
+    and write its launch table: per launch of one iteration, in dispatch
+    order, the kernel, its instances and the floats of the ranges it may
+    read and write (a command's ranges for each of its launches; scratch
+    separate)."""
+    import ad_amd as ad
+    from ad_amd import workloads
+    from ad_amd.device.hip import HIPDevice
+    ad.reset()
+    if config == "c1":
+        workloads.mlp(steps=1, receive=False)
+    elif config == "c3":
+        workloads.layernorm_train(rows=16384, cols=1024, steps=1, receive=False)
+    else:
+        layers, d, h, f, s, b = workloads.TRANSFORMER_CONFIGS[config]
+        workloads.transformer(layers=layers, d_model=d, heads=h, ff=f, seq=s, batch=b, steps=1, receive=False)
+    proc = ad.compile_proc()
+    dev = HIPDevice(use_graphs=False)
+    dev.prepare(proc)
+    loop = dev.loops(proc)[0]
+    table = []
+    for stretch in dev.stretch_graphs[loop.get_proc().id]:
+        for name, count, _, reads, writes, flops in stretch:
+            table.append({"kernel": name, "instances": count, "flops": flops,
+                          "read_floats": _merged_floats([r for r in reads if r[0] != "scratch"]),
+                          "write_floats": _merged_floats([w for w in writes if w[0] != "scratch"]),
+                          "scratch_floats": _merged_floats([r for r in reads + writes if r[0] == "scratch"])})
+    if out_path:
+        with open(out_path, "w") as fh:
+            json.dump(table, fh)
+    log(f"probe {config}: {len(table)} launches per iteration, replaying {iters}")
+    for _ in range(iters):
+        dev.replay(loop, 1)
+        dev.ctx.sync()
+    dev.close()
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -458,7 +516,15 @@ def main():
     ap.add_argument("--eager", action="store_true",
                     help="launch the step's kernels one by one instead of replaying a HIP graph "
                          "(for kernel-trace profilers)")
+    ap.add_argument("--probe", choices=["c1", "c3", "c4", "c5"],
+                    help="only replay this configuration's loop body launch by launch (for kernel traces and "
+                         "counter passes) and write its launch table to --probe-out")
+    ap.add_argument("--probe-iters", type=int, default=3)
+    ap.add_argument("--probe-out", default=None)
     args = ap.parse_args()
+    if args.probe:
+        probe(args.probe, args.probe_iters, args.probe_out)
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}): "

@@ -38,7 +38,7 @@ def _nodes(dev, inner, count):
                 if g == 0:
                     s += 1
                 if makes_node:
-                    _, _, _, reads, writes = stretches[s][g]
+                    _, _, _, reads, writes, _ = stretches[s][g]
                     out.append(("launch", reads, writes))
             elif isinstance(item[1], Receiver):
                 out.extend(("copy",) for _ in item[1].ids)
