@@ -246,6 +246,44 @@ def test_column_reduce_split(hip, rows, cols):
     assert np.array_equal(got["m"], want["m"])
 
 
+def test_wide_streamed_sum(hip, monkeypatch):
+    """A sum of 20 operands, one element per thread with every operand
+    loaded nontemporally (the pass-size threshold lowered to 1 MiB), then
+    scaled: against float64, in the reference's left-to-right order."""
+    from ad_amd.device.hip import codegen
+    monkeypatch.setattr(codegen, "STREAM_PASS_BYTES", 1 << 20)
+    rng = np.random.default_rng(20)
+    xs = [rng.standard_normal((512, 1024)).astype(np.float32) for _ in range(20)]
+    r = Tensor(xs[0])
+    for x in xs[1:]:
+        r = r + Tensor(x)
+    got = {}
+    Receiver(lambda v: got.update(r=v.copy()), [r * 0.5])
+    dev = hip()
+    ad.execute(device=dev)
+    assert any("__builtin_nontemporal_load(" in p.source for ps in dev.kernels.values() for p in ps)
+    want = np.zeros(xs[0].shape, np.float32)
+    for x in xs:
+        want = want + x
+    np.testing.assert_allclose(got["r"], 0.5 * want, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("rows,cols", [(16387, 256), (8193, 512), (4099, 1024), (16384, 1024)])
+def test_row_reduce_ragged_row_counts(hip, rows, cols):
+    """Reductions of short contiguous rows over a row count that leaves the
+    waves' last pass ragged: SUM against float64 (a power-of-two row sums
+    every element), MAX exactly."""
+    rng = np.random.default_rng(rows + cols)
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    X = Tensor(x)
+    got = {}
+    Receiver(lambda a, b: got.update(s=a.copy(), m=b.copy()), [X.sum(-1) * 0.5, X.max(-1)])
+    ad.execute(device=hip())
+    np.testing.assert_allclose(got["s"].reshape(-1), 0.5 * x.astype(np.float64).sum(-1),
+                               rtol=0, atol=cols * np.finfo(np.float32).eps * 4)
+    assert np.array_equal(got["m"].reshape(-1), x.max(-1))
+
+
 @pytest.mark.parametrize("iters", [1, 2, 7, 50, 100])
 def test_feeder_values_reach_every_iteration(hip, iters):
     """A loop accumulates a value fed by the host each iteration (1, 2, ...):

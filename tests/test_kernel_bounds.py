@@ -147,5 +147,24 @@ def test_streamed_accesses_stay_in_bounds(workdir):
     assert "ld4<true>" in open([f for f in _sources(workdir)][0]).read()
 
 
+def test_wide_streamed_pass_stays_in_bounds(workdir, monkeypatch):
+    """A pass of many operands, one element per thread, loading every
+    operand nontemporally (thresholds lowered: 2^12 elements, 17 operands)."""
+    import numpy as np
+    from ad_amd.device.hip import codegen
+    from ad_amd.graph import Receiver, Tensor
+    monkeypatch.setattr(codegen, "SCALAR_MAX_N", 1024)
+    monkeypatch.setattr(codegen, "STREAM_PASS_BYTES", 4096)
+    xs = [Tensor(np.full((64, 64), i, np.float32)) for i in range(17)]
+    r = xs[0]
+    for x in xs[1:]:
+        r = r + x
+    Receiver(lambda v: None, [r * 0.5])
+    ok, log = check_run(ad.compile_proc(), workdir)
+    assert ok, log
+    text = "".join(open(f).read() for f in _sources(workdir))
+    assert text.count("__builtin_nontemporal_load(") >= 17
+
+
 def _sources(workdir):
     return [os.path.join(workdir, f) for f in os.listdir(workdir) if f.endswith(".cpp")]
