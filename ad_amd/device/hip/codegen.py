@@ -260,14 +260,22 @@ def annotate_spans(proc):
                 _note_span(n.kres, n.shape)
 
 
-def _region(km: KMatrix, buffers: BufferInfo):
+def _region(km: KMatrix, buffers: BufferInfo, coarse: bool = False):
+    """``((key, lo, hi), var)``: the floats ``[lo, hi)`` of memory ``key``
+    an access can touch.  An access of a tetris variable is bounded by the
+    variable and, unless ``coarse``, by its span as well (a slice of the
+    variable, such as one head's block of a concatenated result); with an
+    unpacked arena the key is the variable and the range relative to it."""
     var = getattr(km, "tetris_var", None)
+    span = getattr(km, "span", None)
     if var is not None:
         vid, off, size = var
+        lo, hi = off, off + size
+        if span is not None and not coarse and max(lo, span[0]) < min(hi, span[1]):
+            lo, hi = max(lo, span[0]), min(hi, span[1])
         if buffers.unpacked:
-            return (("tv", vid), 0, size), vid
-        return (km.id, off, off + size), vid
-    span = getattr(km, "span", None)
+            return (("tv", vid), lo - off, hi - off), vid
+        return (km.id, lo, hi), vid
     if span is not None:
         return (km.id, span[0], span[1]), ("buf", km.id)
     return (km.id, 0, buffers.size.get(km.id, 1 << 62)), ("buf", km.id)

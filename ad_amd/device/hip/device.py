@@ -282,7 +282,7 @@ class HIPDevice(Device):
                 elif isinstance(c, (Node, FuseBase)) and not isinstance(c, Receiver):
                     for n in ([c] if isinstance(c, Feeder) else nodes(c)):
                         if not n.kres.is_none() and not n.kres.is_temp:
-                            out.add(codegen._region(n.kres, info)[0])
+                            out.add(codegen._region(n.kres, info, coarse=True)[0])
             return out
 
         def scan(body, own):
@@ -297,13 +297,13 @@ class HIPDevice(Device):
                         for km in codegen.iter_kmatrix(k):
                             if km.is_temp or getattr(km, "scratch_offset", None) is not None:
                                 continue
-                            r = codegen._region(km, info)[0]
+                            r = codegen._region(km, info, coarse=True)[0]
                             readers.setdefault(r, set()).add(c.program_id)
                             if own is not None and r not in own:
                                 readers[r].add(None)        # read again every iteration
                             reads.append((km, r))
                     if not n.kres.is_none() and not n.kres.is_temp:
-                        writes.append((n.kres, codegen._region(n.kres, info)[0]))
+                        writes.append((n.kres, codegen._region(n.kres, info, coarse=True)[0]))
         scan(proc, None)
         for km, _ in reads + writes:
             km.stream = False

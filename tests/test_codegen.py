@@ -556,3 +556,22 @@ def test_bf16_plans_compile(M, K, N):
         assert "dp_bf16<256, 128," in product.source
     for p in plans:
         assert len(compile_source(header + p.source)) > 0
+
+
+def test_region_of_a_variable_slice_is_its_span():
+    """An access of a tetris variable conflicts only over the floats its
+    access expression can reach (one head's block of a concatenated result),
+    not over the whole variable; ``coarse`` and an access without a span
+    give the whole variable; unpacked, the range is relative to the
+    variable."""
+    from ad_amd.kernalize import KMatrix
+    k = KMatrix(7, Add(Global(), Val(Constant(1000 + 256))), [256])
+    k.tetris_var = (3, 1000, 1024)
+    codegen._note_span(k, (256,))
+    assert k.span == (1256, 1512)
+    packed, unpacked = codegen.BufferInfo(), codegen.BufferInfo(unpacked=True)
+    assert codegen._region(k, packed) == ((7, 1256, 1512), 3)
+    assert codegen._region(k, packed, coarse=True) == ((7, 1000, 2024), 3)
+    assert codegen._region(k, unpacked) == ((("tv", 3), 256, 512), 3)
+    k.span = None
+    assert codegen._region(k, packed) == ((7, 1000, 2024), 3)
