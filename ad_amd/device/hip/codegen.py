@@ -598,6 +598,60 @@ class _StoreTracker:
             self.stored.append(_region(km, _NO_SIZES)[0])
 
 
+# a left-nested chain of at least this many concat pieces along one index
+# is selected by a balanced tree of comparisons
+CONCAT_BALANCE_MIN = 4
+
+
+def balance_concat(k):
+    """The same operand with every left-nested chain of concats along one
+    index expression (``Concat(Concat(Concat(a, b), c), d)``: conditions
+    ``e > t`` with the same ``e`` and falling thresholds ``t``, as
+    kernalize.make_karg builds them) rebuilt as a balanced tree of
+    comparisons against the same thresholds: each element still reads
+    only the piece whose range holds it, after about log2(n) comparisons
+    instead of up to n.  The concat of a head-by-sample result (128 pieces)
+    otherwise costs up to 128 dependent selects per element.  Operands that
+    are no such chain come back with their pieces balanced."""
+    if not isinstance(k, KConcat) or getattr(k, "balanced", False):
+        return k
+
+    def split(cond):
+        if type(cond) is MoreThan:
+            t = const_of(cond.b)
+            if t is not None:
+                return repr(cond.a), int(t)
+        return None, None
+
+    key, _ = split(k.condition)
+    chain, node = [], k
+    if key is not None:
+        while isinstance(node, KConcat):
+            kk, t = split(node.condition)
+            if kk != key or (chain and t >= chain[-1][0]):
+                break
+            chain.append((t, node.karg_two))
+            node = node.karg_one
+    if len(chain) < CONCAT_BALANCE_MIN:
+        out = KConcat(balance_concat(k.karg_one), balance_concat(k.karg_two), k.condition, k.shape)
+        out.balanced = True
+        return out
+    asc = sorted(chain, key=lambda x: x[0])
+    pieces = [balance_concat(node)] + [balance_concat(p) for _, p in asc]
+    thresholds = [None] + [t for t, _ in asc]
+    e = k.condition.a
+
+    def build(lo, hi):
+        # pieces[j] serves e in (thresholds[j], thresholds[j + 1]]; pieces[0] e <= thresholds[1]
+        if lo == hi:
+            return pieces[lo]
+        mid = (lo + hi + 1) // 2
+        out = KConcat(build(lo, mid - 1), build(mid, hi), MoreThan(e, Val(Constant(thresholds[mid]))), k.shape)
+        out.balanced = True
+        return out
+    return build(0, len(pieces) - 1)
+
+
 class Lowerer:
     """Emits scalar C++ for operands and statements of one kernel.
 
@@ -665,6 +719,7 @@ class Lowerer:
             # access may point outside its buffer for the elements the other
             # piece serves (a slice read as ``(g % n) - c`` underflows below
             # c), so no piece's load is hoisted out of the conditional
+            karg = balance_concat(karg)
             cond = lower_index(karg.condition, self.ity)
             hoist, self.hoist = self.hoist, False
             try:
@@ -944,6 +999,7 @@ def _vector_lines(stmts, ity, params: Params, index_kind="global", hoist=None) -
             lit = f"(float)({const_literal(k.constant)})"
             return f"make_float4({lit}, {lit}, {lit}, {lit})"
         if isinstance(k, KConcat):
+            k = balance_concat(k)
             cond = lower_index(k.condition, ity)
             return f"(({cond}) ? {vec_expr(k.karg_two)} : {vec_expr(k.karg_one)})"
         if k.is_temp:
@@ -1516,6 +1572,7 @@ def _stmt_plan(kind, node, n, index_kind, n_cols, temp_off, stage_off, init_off,
             p = params.ptr("scratch", 0, temp_off[karg.id])
             return f"{p}[_global_id]"
         if isinstance(karg, KConcat):
+            karg = balance_concat(karg)
             cond = lower_index(karg.condition, ity)
             return f"({cond} ? ({operand(karg.karg_two)}) : ({operand(karg.karg_one)}))"
         return _orig(karg)

@@ -575,3 +575,46 @@ def test_region_of_a_variable_slice_is_its_span():
     assert codegen._region(k, unpacked) == ((("tv", 3), 256, 512), 3)
     k.span = None
     assert codegen._region(k, packed) == ((7, 1000, 2024), 3)
+
+
+@pytest.mark.parametrize("pieces", [2, 3, 4, 5, 9, 16, 128])
+def test_balanced_concat_selects_the_same_piece(pieces):
+    """A left-nested chain of concats (kernalize.make_karg's form: the
+    condition of each level is ``e > t`` on the same index, thresholds
+    falling) rebuilt as a balanced tree picks the same piece for every
+    index, with at most ceil(log2(pieces)) + 1 comparisons; a 2-level
+    concat (rows of column chains) balances both levels."""
+    import math
+    from ad_amd.expr import MoreThan, evaluate
+    from ad_amd.kernalize import KConcat, KMatrix
+
+    def chain(e, width, leaf_ids):
+        k = KMatrix(leaf_ids[0], Global(), [1])
+        for i, lid in enumerate(leaf_ids[1:], start=1):
+            k = KConcat(k, KMatrix(lid, Global(), [1]), MoreThan(e, Val(Constant(i * width - 1))), [1])
+        return k
+
+    def select(k, g, depth=0):
+        if isinstance(k, KConcat):
+            hit = evaluate(k.condition, g, 0, 0)
+            return select(k.karg_two if hit else k.karg_one, g, depth + 1)
+        return k.id, depth
+
+    e = Remainder(Global(), Val(Constant(pieces * 7)))
+    orig = chain(e, 7, list(range(pieces)))
+    bal = codegen.balance_concat(orig)
+    for g in range(pieces * 7 * 2):
+        want, _ = select(orig, g)
+        got, depth = select(bal, g)
+        assert got == want
+        if pieces >= codegen.CONCAT_BALANCE_MIN:
+            assert depth <= math.ceil(math.log2(pieces)) + 1
+    # two levels: rows select one of 3 column chains of `pieces` each
+    rows = KConcat(KConcat(chain(e, 7, list(range(100, 100 + pieces))),
+                           chain(e, 7, list(range(200, 200 + pieces))),
+                           MoreThan(Div(Global(), Val(Constant(1000))), Val(Constant(0))), [1]),
+                   chain(e, 7, list(range(300, 300 + pieces))),
+                   MoreThan(Div(Global(), Val(Constant(1000))), Val(Constant(1))), [1])
+    bal2 = codegen.balance_concat(rows)
+    for g in list(range(0, 3000, 13)):
+        assert select(bal2, g)[0] == select(rows, g)[0]
