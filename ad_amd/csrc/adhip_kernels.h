@@ -154,8 +154,9 @@ __device__ __forceinline__ void dp_epilogue(const EPI& epi, adhip_f32x16 (&acc)[
   }
 }
 
-template <int BM, int BN, int SPLIT, int BK, class LA, class LB, class EPI>
+template <int BM, int BN, int SPLIT, int BK, class LA, class LB, class EPI, int NBUF = 2>
 __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& epi, int M, int N, int K) {
+  static_assert(NBUF == 1 || NBUF == 2, "one or two LDS panel buffers");
   static_assert(BM % 64 == 0 && BN % 64 == 0, "tile must be a multiple of 64");
   static_assert(BK % 16 == 0, "K panel must be a multiple of 16");
   constexpr int TM = BM / 64, TN = BN / 64;              // 32x32 tiles per wave
@@ -174,7 +175,7 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
   constexpr bool AR = LA::kMode == 0, BR = LB::kMode == 1;
   constexpr int KP = BK + 4, H = BK / 2;
   constexpr int APITCH = AR ? KP : BM + 4, BPITCH = BR ? KP : BN + 4;
-  constexpr int A_FLOATS = 2 * (AR ? BM : BK) * APITCH, B_FLOATS = 2 * (BR ? BN : BK) * BPITCH;
+  constexpr int A_FLOATS = NBUF * (AR ? BM : BK) * APITCH, B_FLOATS = NBUF * (BR ? BN : BK) * BPITCH;
   constexpr int C_FLOATS = EPI::kVec4 ? 4 * 32 * DP_CPITCH : 0;
   constexpr int S_FLOATS = A_FLOATS + B_FLOATS > C_FLOATS ? A_FLOATS + B_FLOATS : C_FLOATS;
   __shared__ __attribute__((aligned(16))) float smem[S_FLOATS];
@@ -290,6 +291,10 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
   // Two LDS buffers: the panel prefetched into registers during the
   // products of the current panel is stored into the other buffer, so one
   // barrier per panel separates every write of a buffer from its last read.
+  // One buffer (NBUF = 1): half the LDS, so a deeper panel still leaves
+  // two blocks per compute unit; the next panel (already in registers) is
+  // stored once every wave is done with the current one, a second barrier
+  // per panel.
   const int lk = lane >> 5, lr = lane & 31;
   if (kbeg < kend) {
     load_a(kbeg);
@@ -348,12 +353,21 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
               acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][st], bf[j][st], acc[i][j], 0, 0, 0);
       }
       __builtin_amdgcn_s_setprio(0);
-      if (more) {
-        store_a(cur ^ 1);
-        store_b(cur ^ 1);
+      if constexpr (NBUF == 2) {
+        if (more) {
+          store_a(cur ^ 1);
+          store_b(cur ^ 1);
+        }
+        __syncthreads();
+        cur ^= 1;
+      } else {
+        if (more) {
+          __syncthreads();
+          store_a(0);
+          store_b(0);
+        }
+        __syncthreads();
       }
-      __syncthreads();
-      cur ^= 1;
     }
   }
   dp_epilogue<BM, BN>(epi, acc, smem, m0, n0, M, N, chunk);

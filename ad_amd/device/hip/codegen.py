@@ -1201,6 +1201,15 @@ def dp_config(M, N, K):
     return BM, BN, split, dp_panel(M, N, K, BM, BN, split)
 
 
+def dp_buffers(M, N, K, BM, BN, split, BK):
+    """LDS buffers of the K panels: one for 128 x 128 tiles (the next panel
+    stored after a second barrier; measured three times each on one box:
+    4096^3 DotProd+Elw 112.0 -> 114.4 TFLOP/s, C5 60.36 -> 60.91 steps/s),
+    two for smaller tiles (the next panel stored while the current one is
+    read; one buffer gained nothing on the K = 64 products)."""
+    return 1 if BM == 128 and BN == 128 else 2
+
+
 def dp_panel(M, N, K, BM, BN, split):
     """Depth of the K panels staged in LDS: 32 (measured against 16, 48 and
     64 at 4096^3 and on the C5 step: 32 halves the barriers per product of
@@ -1301,9 +1310,11 @@ def dotprod_plan(stmts, dp, A=None, B=None, config=None, partial_off=None) -> Ke
                           flops=2 * M * N * K)
     epi = _dp_epi_struct(stmts, params, ity, M, N, partial_off)
     init = _init_list(params)
+    nbuf = dp_buffers(M, N, K, BM, BN, split, BK)
+    tmpl = f"{BM}, {BN}, {split}, {BK}" + (", LA, LB, EPI, 1" if nbuf == 1 else "")
     src = ((la + lb + epi).replace("@FIELDS@", _fields(params)) +
            f"extern \"C\" __global__ void __launch_bounds__(256) {KNAME}({_params_decl(params)}) {{\n"
-           f"  adhip::dp_mfma<{BM}, {BN}, {split}, {BK}>(LA{{{init}}}, LB{{{init}}}, EPI{{{init}}}, {M}, {N}, {K});\n}}\n")
+           f"  adhip::dp_mfma<{tmpl}>(LA{{{init}}}, LB{{{init}}}, EPI{{{init}}}, {M}, {N}, {K});\n}}\n")
     grid = (ceil(N / BN), ceil(M / BM) * split, 1)
     return KernelPlan(src, grid, (256, 1, 1), _plan_args(params), family="dotprod",
                       flops=2 * M * N * K)

@@ -89,6 +89,39 @@ def _time_launches(dev, cmds, reps, warmup=2):
     return dev.ctx.elapsed_ms(10, 11) / reps
 
 
+def vendor_gemm(reps):
+    """The 4096^3 fp32 product on the vendor BLAS (torch.matmul, reduced
+    precision paths off), timed with torch's events: a reference point for
+    the DotProd+Elw kernel, not part of the backend.  Runs in a child
+    interpreter: a process that has loaded libadhip.so has the system HIP
+    runtime mapped, and torch's own runtime then finds no device."""
+    import subprocess
+    code = r"""
+import json, torch
+torch.backends.cuda.matmul.allow_tf32 = False
+torch.backends.cuda.matmul.allow_fp16_reduced_precision_reduction = False
+n, reps = 4096, %d
+g = torch.Generator(device="cuda").manual_seed(0)
+a = torch.randn(n, n, device="cuda", generator=g)
+b = torch.randn(n, n, device="cuda", generator=g)
+for _ in range(3):
+    c = a @ b
+torch.cuda.synchronize()
+s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+s.record()
+for _ in range(reps):
+    c = a @ b
+e.record(); e.synchronize()
+ms = s.elapsed_time(e) / reps
+print(json.dumps({"vendor_gemm_4096": {"library": "torch.matmul fp32 (hipBLASLt/rocBLAS), TF32 off", "ms": round(ms, 4),
+                                        "tflops": round(2 * n ** 3 / ms / 1e9, 2)}}))
+""" % reps
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=600)
+    if out.returncode != 0:
+        raise RuntimeError(out.stderr[-2000:])
+    return json.loads(out.stdout.strip().splitlines()[-1])
+
+
 def micro_dotprod(reps, dot="fp32"):
     """The 4096^3 DotProd+Elw command; with ``dot="bf16"`` its time includes
     the two operand-packing kernels."""
@@ -520,8 +553,13 @@ def main():
                     help="only replay this configuration's loop body launch by launch (for kernel traces and "
                          "counter passes) and write its launch table to --probe-out")
     ap.add_argument("--probe-iters", type=int, default=3)
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="only time the 4096^3 fp32 product on the vendor BLAS through torch (a reference point)")
     ap.add_argument("--probe-out", default=None)
     args = ap.parse_args()
+    if args.vendor_gemm:
+        print(json.dumps(vendor_gemm(args.micro_reps)), flush=True)
+        return
     if args.probe:
         probe(args.probe, args.probe_iters, args.probe_out)
         return

@@ -7,6 +7,7 @@ replay, Feeder staging, in-loop Receivers), several devices in one process
 and a device reused for a second program; a run with the host arena cut
 one float short shows the check catches an access past its end."""
 import os
+import re
 import shutil
 
 import pytest
@@ -132,6 +133,22 @@ def test_bf16_products_stay_in_bounds(workdir, M, K, N):
     Receiver(lambda v: None, [((a @ b.T()) + bias).sigmoid()])
     ok, log = check_run(ad.compile_proc(), workdir, dot_precision="bf16", bf16_min_macs=0)
     assert ok, log
+
+
+@pytest.mark.parametrize("M,K,N,ta", [(640, 1024, 520, False), (300, 2048, 1000, True)])
+def test_single_buffer_tiles_stay_in_bounds(workdir, M, K, N, ta):
+    """128 x 128 tiles stage their K panels in one LDS buffer (ragged M, N
+    and transposed A)."""
+    import numpy as np
+    from ad_amd.graph import Receiver, Tensor
+    rng = np.random.default_rng(M + K + N)
+    a = Tensor(rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32))
+    b = Tensor(rng.standard_normal((K, N)).astype(np.float32))
+    Receiver(lambda v: None, [((a.T() if ta else a) @ b).sigmoid()])
+    ok, log = check_run(ad.compile_proc(), workdir)
+    assert ok, log
+    text = "".join(open(f).read() for f in _sources(workdir))
+    assert re.search(r"dp_mfma<128, 128, \d+, 32, LA, LB, EPI, 1>", text)
 
 
 def test_streamed_accesses_stay_in_bounds(workdir):
