@@ -1202,19 +1202,24 @@ def dp_config(M, N, K):
 
 
 def dp_buffers(M, N, K, BM, BN, split, BK):
-    """LDS buffers of the K panels: one for 128 x 128 tiles (the next panel
-    stored after a second barrier; measured three times each on one box:
-    4096^3 DotProd+Elw 112.0 -> 114.4 TFLOP/s, C5 60.36 -> 60.91 steps/s),
-    two for smaller tiles (the next panel stored while the current one is
-    read; one buffer gained nothing on the K = 64 products)."""
-    return 1 if BM == 128 and BN == 128 else 2
+    """LDS buffers of the K panels: one for 128 x 128 and 64 x 64 tiles (the
+    next panel, already in registers, stored after a second barrier; three
+    alternating runs on one box: 4096^3 DotProd+Elw 112.0 -> 114.4
+    TFLOP/s, C5 60.36 -> 60.91 steps/s for the 128 x 128 tiles; with 64-deep
+    panels for the 64 x 64 tiles, two runs each: C5 61.0 -> 62.1, C4 643 ->
+    652 steps/s), two for the mixed 128 x 64 tiles (the next panel stored
+    while the current one is read)."""
+    return 1 if BM == BN else 2
 
 
 def dp_panel(M, N, K, BM, BN, split):
-    """Depth of the K panels staged in LDS: 32 (measured against 16, 48 and
-    64 at 4096^3 and on the C5 step: 32 halves the barriers per product of
-    16 and still leaves two blocks per compute unit)."""
-    return 32
+    """Depth of the K panels staged in LDS: 32 for 128-wide tiles (measured
+    against 16, 48 and 64 at 4096^3 and on the C5 step: 32 halves the
+    barriers per product of 16 and still leaves two blocks per compute
+    unit), 64 for 64 x 64 tiles in one buffer (35 KB per block; 16- and
+    32-deep panels measured slower on the C5 step: 59.5 and 61.7 against
+    62.1 steps/s)."""
+    return 64 if BM == 64 and BN == 64 else 32
 
 
 VEC_HOIST_MAX = 4

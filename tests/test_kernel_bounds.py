@@ -135,10 +135,13 @@ def test_bf16_products_stay_in_bounds(workdir, M, K, N):
     assert ok, log
 
 
-@pytest.mark.parametrize("M,K,N,ta", [(640, 1024, 520, False), (300, 2048, 1000, True)])
-def test_single_buffer_tiles_stay_in_bounds(workdir, M, K, N, ta):
-    """128 x 128 tiles stage their K panels in one LDS buffer (ragged M, N
-    and transposed A)."""
+@pytest.mark.parametrize("M,K,N,ta,tile", [(640, 1024, 520, False, 128), (300, 2048, 1000, True, 128),
+                                           (300, 2048, 64, False, 64), (130, 64, 257, True, 64),
+                                           (512, 512, 64, False, 64)])
+def test_single_buffer_tiles_stay_in_bounds(workdir, M, K, N, ta, tile):
+    """128 x 128 tiles (32-deep panels) and 64 x 64 tiles (64-deep) stage
+    their K panels in one LDS buffer (ragged M, N and K, K splits,
+    transposed A)."""
     import numpy as np
     from ad_amd.graph import Receiver, Tensor
     rng = np.random.default_rng(M + K + N)
@@ -148,7 +151,7 @@ def test_single_buffer_tiles_stay_in_bounds(workdir, M, K, N, ta):
     ok, log = check_run(ad.compile_proc(), workdir)
     assert ok, log
     text = "".join(open(f).read() for f in _sources(workdir))
-    assert re.search(r"dp_mfma<128, 128, \d+, 32, LA, LB, EPI, 1>", text)
+    assert re.search(rf"dp_mfma<{tile}, {tile}, \d+, {32 if tile == 128 else 64}, LA, LB, EPI, 1>", text)
 
 
 def test_streamed_accesses_stay_in_bounds(workdir):
