@@ -373,6 +373,174 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
   dp_epilogue<BM, BN>(epi, acc, smem, m0, n0, M, N, chunk);
 }
 
+// dp_quad<SPLIT>: a DotProd for launches too small to fill the device (a few
+// per-head products of 512 terms, one split weight gradient).  A 64x64 tile
+// per block leaves most compute units idle there, and each wave's chain of
+// K/2 dependent MFMAs sets the launch's time.  Here a block of 4 waves takes
+// a 32x32 output tile and splits each 128-deep K panel among its waves (wave
+// w takes panel columns 32w .. 32w+31): four times the blocks, each wave's
+// chain a quarter as long.  Panels are staged in one LDS buffer with the
+// next panel prefetched into registers (two barriers per panel), laid out
+// as in dp_mfma.  At the end the four 32x32 partial tiles go through LDS and
+// each thread adds its 4 consecutive elements of one row in wave order, then
+// runs the epilogue on them (float4 interface when EPI::kVec4, else per
+// element).  SPLIT > 1 splits K into chunks over blockIdx.y as in dp_mfma.
+constexpr int DPQ_BK = 128, DPQ_RPITCH = 36;
+
+template <int SPLIT, class LA, class LB, class EPI>
+__device__ __forceinline__ void dp_quad(const LA& la, const LB& lb, const EPI& epi, int M, int N, int K) {
+  constexpr int BT = 32, BK = DPQ_BK, KW = BK / 4, H = KW / 2;
+  constexpr int V = BT * BK / 4 / 256;                // float4 loads per thread per operand
+  constexpr bool AR = LA::kMode == 0, BR = LB::kMode == 1;
+  constexpr int KP = BK + 4;
+  constexpr int APITCH = AR ? KP : BT + 4, BPITCH = BR ? KP : BT + 4;
+  constexpr int A_FLOATS = (AR ? BT : BK) * APITCH, B_FLOATS = (BR ? BT : BK) * BPITCH;
+  constexpr int R_FLOATS = 4 * BT * DPQ_RPITCH;
+  constexpr int S_FLOATS = A_FLOATS + B_FLOATS > R_FLOATS ? A_FLOATS + B_FLOATS : R_FLOATS;
+  __shared__ __attribute__((aligned(16))) float smem[S_FLOATS];
+  float* const As = smem;
+  float* const Bs = smem + A_FLOATS;
+  auto a_off = [](int m, int k) { return AR ? m * APITCH + k : k * APITCH + m; };
+  auto b_off = [](int n, int k) { return BR ? n * BPITCH + k : k * BPITCH + n; };
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tiles_m = (M + BT - 1) / BT;
+  int bx, by;
+  dp_block_tile(bx, by);
+  const int chunk = SPLIT > 1 ? by / tiles_m : 0;
+  const int m0 = (SPLIT > 1 ? by % tiles_m : by) * BT, n0 = bx * BT;
+  int kbeg = 0, kend = K;
+  if constexpr (SPLIT > 1) {
+    const int kc = ((K + SPLIT - 1) / SPLIT + BK - 1) / BK * BK;
+    kbeg = chunk * kc;
+    kend = kbeg + kc < K ? kbeg + kc : K;
+  }
+  float ra[V][4], rb[V][4];
+  // float4 v of a panel: (row, k) of its first float
+  auto a_pos = [](int v, int& m, int& k) {
+    if constexpr (AR) { m = v / (BK / 4); k = 4 * (v % (BK / 4)); }
+    else { k = v / (BT / 4); m = 4 * (v % (BT / 4)); }
+  };
+  auto b_pos = [](int v, int& n, int& k) {
+    if constexpr (BR) { n = v / (BK / 4); k = 4 * (v % (BK / 4)); }
+    else { k = v / (BT / 4); n = 4 * (v % (BT / 4)); }
+  };
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      int m, n, ka, kb;
+      a_pos(tid + 256 * i, m, ka);
+      b_pos(tid + 256 * i, n, kb);
+      m += m0; ka += k0; n += n0; kb += k0;
+      if constexpr (LA::kVec) {
+        const float4 x = (m < M && ka < kend) ? la.at4(m, ka) : make_float4(0.f, 0.f, 0.f, 0.f);
+        ra[i][0] = x.x; ra[i][1] = x.y; ra[i][2] = x.z; ra[i][3] = x.w;
+      } else if constexpr (AR) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ra[i][j] = (m < M && ka + j < kend) ? la.at(m, ka + j) : 0.f;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ra[i][j] = (ka < kend && m + j < M) ? la.at(m + j, ka) : 0.f;
+      }
+      if constexpr (LB::kVec) {
+        const float4 x = (n < N && kb < kend) ? lb.at4(kb, n) : make_float4(0.f, 0.f, 0.f, 0.f);
+        rb[i][0] = x.x; rb[i][1] = x.y; rb[i][2] = x.z; rb[i][3] = x.w;
+      } else if constexpr (BR) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) rb[i][j] = (n < N && kb + j < kend) ? lb.at(kb + j, n) : 0.f;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) rb[i][j] = (kb < kend && n + j < N) ? lb.at(kb, n + j) : 0.f;
+      }
+    }
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      int m, n, ka, kb;
+      a_pos(tid + 256 * i, m, ka);
+      b_pos(tid + 256 * i, n, kb);
+      *reinterpret_cast<float4*>(As + a_off(m, ka)) = make_float4(ra[i][0], ra[i][1], ra[i][2], ra[i][3]);
+      *reinterpret_cast<float4*>(Bs + b_off(n, kb)) = make_float4(rb[i][0], rb[i][1], rb[i][2], rb[i][3]);
+    }
+  };
+
+  adhip_f32x16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+  const int lk = lane >> 5, lr = lane & 31;
+  if (kbeg < kend) {
+    load(kbeg);
+    store();
+    __syncthreads();
+    for (int k0 = kbeg; k0 < kend; k0 += BK) {
+      const bool more = k0 + BK < kend;
+      if (more) load(k0 + BK);
+      // MFMA step s of the wave's 32 panel columns multiplies column
+      // KW * wave + H * (lane / 32) + s (the same assignment for A and B)
+#pragma unroll
+      for (int q = 0; q < H / 4; ++q) {
+        float af[4], bf[4];
+        const int kk = KW * wave + H * lk + 4 * q;
+        if constexpr (AR) {
+          const float4 x = *reinterpret_cast<const float4*>(As + a_off(lr, kk));
+          af[0] = x.x; af[1] = x.y; af[2] = x.z; af[3] = x.w;
+        } else {
+#pragma unroll
+          for (int st = 0; st < 4; ++st) af[st] = As[a_off(lr, kk + st)];
+        }
+        if constexpr (BR) {
+          const float4 x = *reinterpret_cast<const float4*>(Bs + b_off(lr, kk));
+          bf[0] = x.x; bf[1] = x.y; bf[2] = x.z; bf[3] = x.w;
+        } else {
+#pragma unroll
+          for (int st = 0; st < 4; ++st) bf[st] = Bs[b_off(lr, kk + st)];
+        }
+#pragma unroll
+        for (int st = 0; st < 4; ++st) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[st], bf[st], acc, 0, 0, 0);
+      }
+      if (more) {
+        __syncthreads();
+        store();
+      }
+      __syncthreads();
+    }
+  }
+  // the four waves' partial tiles: lane holds column lane % 32 and rows
+  // 8*(r/4) + 4*(lane/32) + r%4 of its wave's tile
+  __syncthreads();
+  float* const red = smem;
+#pragma unroll
+  for (int r = 0; r < 16; ++r)
+    red[(wave * BT + 8 * (r >> 2) + 4 * lk + (r & 3)) * DPQ_RPITCH + lr] = acc[r];
+  __syncthreads();
+  const int row = tid >> 3, c4 = 4 * (tid & 7);
+  float4 v = *reinterpret_cast<const float4*>(red + row * DPQ_RPITCH + c4);
+#pragma unroll
+  for (int w = 1; w < 4; ++w) {
+    const float4 x = *reinterpret_cast<const float4*>(red + (w * BT + row) * DPQ_RPITCH + c4);
+    v.x = v.x + x.x; v.y = v.y + x.y; v.z = v.z + x.z; v.w = v.w + x.w;
+  }
+  const int gm = m0 + row, gn = n0 + c4;
+  if (gm >= M) return;
+  constexpr int NL = EPI::kLoads > 0 ? EPI::kLoads : 1;
+  if constexpr (EPI::kVec4) {
+    if (gn < N) {
+      float4 lv[NL];
+      epi.load4(gm, gn, lv);
+      epi.vec(v, gm, gn, chunk, lv);
+    }
+  } else {
+    const float vs[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (gn + j < N) {
+        float lv[NL];
+        epi.load(gm, gn + j, lv);
+        epi(vs[j], gm, gn + j, chunk, lv);
+      }
+  }
+}
+
 // dp_skinny<MR>: a DotProd with at most MR rows (a product like [2,255] x
 // [255,255], where an MFMA tile would idle on the short side and its K
 // panels and barriers would set the time).  A block of 256 lanes takes 16

@@ -71,6 +71,9 @@ class KernelPlan:
     reads: Optional[list] = None  # ranges read / written, when narrower than the command's
     writes: Optional[list] = None
     scratch: Tuple[int, int] = (0, 0)   # [lo, hi) of the command's scratch floats it touches
+    # the same work on the ``dp_quad`` kernel (same arguments, ranges and
+    # results layout), taken by launches too small to fill the device
+    narrow: Optional["KernelPlan"] = None
 
     def __post_init__(self):
         # register temps are named after node ids; number them by first use
@@ -1285,6 +1288,28 @@ def _dp_epi_struct(stmts, params: Params, ity, M, N, partial_off=None, allow_vec
 # most this many terms per output ``dp_direct`` (no MFMA tile)
 SKINNY_M, DIRECT_K = 8, 8
 
+# ``dp_quad``: 32 x 32 tiles, 128-deep panels split among a block's 4 waves
+QUAD_TILE, QUAD_PANEL = 32, 128
+# a product on 64 x 64 tiles whose K chunks have at least this many terms
+# gets a ``dp_quad`` alternative; a launch group takes it when its 64 x 64
+# blocks (all instances) number at most NARROW_MAX_BLOCKS, i.e. half the
+# compute units or fewer: there it runs four times the waves on chains a
+# quarter as long, and past that the wider tile's lower operand traffic
+# per flop wins
+QUAD_MIN_CHUNK, NARROW_MAX_BLOCKS = 256, 128
+
+
+def quad_eligible(M, N, K, config) -> bool:
+    """A 64 x 64-tile fp32 product long enough in K for ``dp_quad``."""
+    BM, BN, split, _ = config
+    return BM == 64 and BN == 64 and M > SKINNY_M and K > DIRECT_K and \
+        ceil(K / split) >= QUAD_MIN_CHUNK
+
+
+def use_narrow(plan: "KernelPlan", instances: int) -> bool:
+    """A launch group of ``instances`` copies of ``plan`` runs ``plan.narrow``."""
+    return plan.narrow is not None and plan.grid[0] * plan.grid[1] * instances <= NARROW_MAX_BLOCKS
+
 
 def dotprod_plan(stmts, dp, A=None, B=None, config=None, partial_off=None) -> KernelPlan:
     """DotProd (+ elementwise epilogue) on fp32 MFMA tiles
@@ -1318,6 +1343,14 @@ def dotprod_plan(stmts, dp, A=None, B=None, config=None, partial_off=None) -> Ke
                           flops=2 * M * N * K)
     epi = _dp_epi_struct(stmts, params, ity, M, N, partial_off)
     init = _init_list(params)
+    if BM == QUAD_TILE:
+        assert BN == QUAD_TILE and BK == QUAD_PANEL, "dp_quad takes 32 x 32 tiles and 128-deep panels"
+        src = ((la + lb + epi).replace("@FIELDS@", _fields(params)) +
+               f"extern \"C\" __global__ void __launch_bounds__(256) {KNAME}({_params_decl(params)}) {{\n"
+               f"  adhip::dp_quad<{split}>(LA{{{init}}}, LB{{{init}}}, EPI{{{init}}}, {M}, {N}, {K});\n}}\n")
+        grid = (ceil(N / QUAD_TILE), ceil(M / QUAD_TILE) * split, 1)
+        return KernelPlan(src, grid, (256, 1, 1), _plan_args(params), family="dotprod",
+                          flops=2 * M * N * K)
     nbuf = dp_buffers(M, N, K, BM, BN, split, BK)
     tmpl = f"{BM}, {BN}, {split}, {BK}" + (", LA, LB, EPI, 1" if nbuf == 1 else "")
     src = ((la + lb + epi).replace("@FIELDS@", _fields(params)) +
@@ -1749,7 +1782,7 @@ def command_plans(cmd, buffers: BufferInfo, scratch_base: int, opts: PlanOptions
             ps, need = phased_plans(stmts_run, pairs, n, kind, cols, init, end + snap, opts)
         ps, need = copies + ps, need + snap
         reads, writes = stmt_regions(group, buffers) if len(groups) > 1 else (None, None)
-        for p in ps:
+        for p in ps + [p.narrow for p in ps if p.narrow is not None]:
             p.reads, p.writes = reads, writes
             p.scratch = (end - scratch_base, end - scratch_base + need)
         plans.extend(ps)
@@ -1857,10 +1890,17 @@ def first_pass_plans(part, n, init_node, alloc: ScratchAlloc, opts=DEFAULT_OPTIO
             off = alloc.take(K * N)
             pre.append(gather_plan(B, K, N, off))
             B = _dense_scratch_operand(off, N)
+        quad = (QUAD_TILE, QUAD_TILE, cfg[2], QUAD_PANEL) if quad_eligible(M, N, K, cfg) else None
+
+        def with_narrow(main, stmts, poff=None):
+            if quad is not None:
+                main.narrow = dotprod_plan(stmts, init_node, A, B, quad, partial_off=poff)
+                assert main.narrow.args == main.args, "dp_quad alternative with other arguments"
+            return main
         if cfg[2] == 1 and epilogue_loads(part) <= EPILOGUE_MAX_LOADS:
-            return pre + [dotprod_plan(part, init_node, A, B, cfg)]
+            return pre + [with_narrow(dotprod_plan(part, init_node, A, B, cfg), part)]
         poff = alloc.take(cfg[2] * M * N)
-        main = dotprod_plan([], init_node, A, B, cfg, partial_off=poff)
+        main = with_narrow(dotprod_plan([], init_node, A, B, cfg, partial_off=poff), [], poff)
         comb = elementwise_plan([("sum", (poff, cfg[2], M * N, 0, False))] + part, M * N,
                                 index_kind="dp", n_cols=N, init_value="_value")
         return pre + [main, comb]

@@ -135,7 +135,12 @@ class HIPDevice(Device):
       bytes that no other command reads (and no loop iteration reads again),
       and writes of such a range no command reads, bypass the caches
       (nontemporal), so they do not evict data that is read again (None:
-      never).  Results are unchanged.
+      never).  Results are unchanged;
+    * ``narrow_launches`` -- a launch group of 64 x 64-tile products too
+      small to fill the device (at most ``codegen.NARROW_MAX_BLOCKS`` blocks)
+      runs the ``dp_quad`` kernel instead: 32 x 32 tiles, each block's K
+      panels split among its four waves.  Sums are grouped differently
+      (within the fp32 tolerance of any K split).
     """
 
     def __init__(self, device_index: int = 0, use_graphs: bool = True, jit_threads: int = None,
@@ -143,8 +148,9 @@ class HIPDevice(Device):
                  exact_reduce: bool = False, feeder_offset_zero: bool = False,
                  strict_temps: bool = False, dot_precision: str = "fp32", bf16_min_macs: int = 1 << 30,
                  loop_unroll: int = 32, arena: str = "packed", stream_min_bytes: int = 32 << 20,
-                 graph_dag: bool = False):
+                 graph_dag: bool = False, narrow_launches: bool = True):
         super().__init__()
+        self.narrow_launches = narrow_launches
         self.graph_dag = graph_dag
         assert arena in ("packed", "unpacked"), "arena must be packed or unpacked"
         assert not (arena == "unpacked" and feeder_offset_zero), \
@@ -197,6 +203,7 @@ class HIPDevice(Device):
         self._schedules = {}         # Proc id -> one-lane items (captured into graphs)
         self.stretch_graphs = {}     # Proc id -> per stretch, per launch group: (kernel, instances, deps, reads, writes, flops)
         self._lane_schedules = {}    # Proc id -> items over self.lanes lanes (uncaptured runs)
+        self._narrow_plans = {}      # kernel name -> dp_quad plan some launch group takes
         self._capturing = False
         self.stats = {"kernels": 0, "unique_sources": 0, "multipass_cmds": 0, "launches_per_iter": 0}
 
@@ -418,7 +425,7 @@ class HIPDevice(Device):
             for i, (is_ptr, v) in enumerate(vals):
                 table[boff // 8 + i] = (base + v) if is_ptr else v
         self.ctx.write(self.table_off, table)
-        funcs = self._compile(plans)
+        funcs = self._compile({**plans, "narrow": list(self._narrow_plans.values())})
         self.stats["unique_sources"] += len(funcs)
         tbase = self.ctx.base + self.table_off
         for pid, ps in plans.items():
@@ -520,8 +527,16 @@ class HIPDevice(Device):
                 rows, plans_of = [], []
                 for group in groups:
                     members = [launches[i] for i in group]
-                    plans_of.append((members[0].plan, len(members)))
-                    rows.append(add_rows([self._arg_values(m.plan, m.cmd.program_id) for m in members]))
+                    plan = members[0].plan
+                    # a group too small to fill the device takes the plans'
+                    # dp_quad alternative (same arguments, same results)
+                    narrow = self.narrow_launches and codegen.use_narrow(plan, len(members))
+                    if narrow:
+                        plan = plan.narrow
+                        self._narrow_plans[plan.name] = plan
+                    plans_of.append((plan, len(members)))
+                    rows.append(add_rows([self._arg_values(m.plan.narrow if narrow else m.plan, m.cmd.program_id)
+                                          for m in members]))
                 # the launch groups of this stretch and the earlier groups each
                 # must follow (kernel name, instances, dependencies)
                 self.stretch_graphs.setdefault(p.id, []).append(

@@ -57,6 +57,54 @@ def test_dotprod_shapes(hip, M, K, N, ta, tb):
     np.testing.assert_allclose(got["r"], ref, rtol=0, atol=bound)
 
 
+@pytest.mark.parametrize("M,K,N,ta,tb,copies", [(300, 2048, 64, False, False, 1), (130, 300, 257, True, True, 1),
+                                                (512, 512, 64, False, False, 3), (96, 1000, 100, False, True, 1),
+                                                (64, 260, 36, True, False, 2), (512, 512, 64, True, True, 16)])
+def test_narrow_launch_parity(hip, M, K, N, ta, tb, copies):
+    """Launch groups too small to fill the device run ``dp_quad`` (32 x 32
+    tiles, each block's K panels split among its four waves, partial tiles
+    added through LDS): the pre-activation ``A@B + bias`` of every product
+    against float64 within sqrt(K)·eps·Σ_k|a||b| per element, the sigmoid
+    epilogue against the float64 sigmoid of the received pre-activation,
+    and the whole output against the 64 x 64-tile kernel's (narrow
+    launches off) within fp32 rounding of a regrouped sum."""
+    rng = np.random.default_rng(M + K + N + copies)
+    data = []
+    for _ in range(copies):
+        a = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+        b = rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+        data.append((a, b, rng.standard_normal((N,)).astype(np.float32)))
+
+    def build():
+        outs, got = [], {}
+        for a, b, bias in data:
+            A, B, C = Tensor(a), Tensor(b), Tensor(bias)
+            pre = (A.T() if ta else A) @ (B.T() if tb else B) + C
+            outs += [pre, pre.sigmoid()]
+        Receiver(lambda *v: got.setdefault("v", [x.copy() for x in v]), outs)
+        return got
+
+    runs = {}
+    for narrow in (True, False):
+        ad.reset()
+        got = build()
+        dev = hip(narrow_launches=narrow)
+        ad.execute(device=dev)
+        names = " ".join(p.source for p in dev._narrow_plans.values())
+        assert ("dp_quad" in names) == narrow
+        runs[narrow] = got["v"]
+    eps = np.finfo(np.float32).eps
+    for i, (a, b, bias) in enumerate(data):
+        a64 = (a.T if ta else a).astype(np.float64)
+        b64 = (b.T if tb else b).astype(np.float64)
+        ref = a64 @ b64 + bias
+        bound = np.sqrt(K) * eps * (np.abs(a64) @ np.abs(b64)) + 4 * eps * np.abs(bias)
+        pre, sig = runs[True][2 * i], runs[True][2 * i + 1]
+        assert np.all(np.abs(pre - ref) <= bound), f"product {i}: {np.max(np.abs(pre - ref) / bound):.3f} x bound"
+        np.testing.assert_allclose(sig, 1 / (1 + np.exp(-pre.astype(np.float64))), rtol=1e-5, atol=1e-6)
+        np.testing.assert_allclose(pre, runs[False][2 * i], rtol=0, atol=float(np.max(bound)))
+
+
 def test_reference_known_answers_dotprod(hip):
     """tests/dotprod_test.py:8-9 of the reference (torch seed 42 inputs)."""
     d = np.load(GOLDEN / "dotprod_test_inputs.npz")

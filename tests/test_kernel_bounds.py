@@ -148,10 +148,34 @@ def test_single_buffer_tiles_stay_in_bounds(workdir, M, K, N, ta, tile):
     a = Tensor(rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32))
     b = Tensor(rng.standard_normal((K, N)).astype(np.float32))
     Receiver(lambda v: None, [((a.T() if ta else a) @ b).sigmoid()])
-    ok, log = check_run(ad.compile_proc(), workdir)
+    ok, log = check_run(ad.compile_proc(), workdir, narrow_launches=False)
     assert ok, log
     text = "".join(open(f).read() for f in _sources(workdir))
     assert re.search(rf"dp_mfma<{tile}, {tile}, \d+, {32 if tile == 128 else 64}, LA, LB, EPI, 1>", text)
+
+
+@pytest.mark.parametrize("M,K,N,ta,tb,copies", [(300, 2048, 64, False, False, 1), (130, 300, 257, True, True, 1),
+                                                (512, 512, 64, False, False, 3), (96, 1000, 100, False, True, 1),
+                                                (64, 260, 36, True, False, 2)])
+def test_narrow_launches_stay_in_bounds(workdir, M, K, N, ta, tb, copies):
+    """Launch groups too small to fill the device run ``dp_quad`` (32 x 32
+    tiles, 128-deep panels split among the waves): ragged M, N and K, K
+    splits, transposed operands, float4 and scalar epilogues, several
+    products in one launch."""
+    import numpy as np
+    from ad_amd.graph import Receiver, Tensor
+    rng = np.random.default_rng(M + K + N + copies)
+    outs = []
+    for _ in range(copies):
+        a = Tensor(rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32))
+        b = Tensor(rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32))
+        bias = Tensor(rng.standard_normal((N,)).astype(np.float32))
+        outs.append(((a.T() if ta else a) @ (b.T() if tb else b) + bias).sigmoid())
+    Receiver(lambda *v: None, outs)
+    ok, log = check_run(ad.compile_proc(), workdir)
+    assert ok, log
+    text = "".join(open(f).read() for f in _sources(workdir))
+    assert re.search(r"dp_quad<\d+>", text) and not re.search(r"dp_mfma<64, 64,", text)
 
 
 def test_streamed_accesses_stay_in_bounds(workdir):
