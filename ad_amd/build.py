@@ -59,8 +59,9 @@ extern "C" __global__ void __launch_bounds__(256) probe_dp_narrow(float* a) { ad
 extern "C" __global__ void __launch_bounds__(256) probe_dp_small(float* a) { adhip::dp_mfma<64, 64, 2, 16>(LA{a}, LB{a}, EPI{a}, 64, 64, 64); }
 extern "C" __global__ void __launch_bounds__(256) probe_dp_vec(float* a) { adhip::dp_mfma<128, 64, 1, 16>(LA{a}, LB{a}, EP4{a}, 64, 64, 64); }
 extern "C" __global__ void __launch_bounds__(256) probe_dp_vec_small(float* a) { adhip::dp_mfma<64, 64, 4, 64>(LA{a}, LB{a}, EP4{a}, 64, 64, 64); }
-extern "C" __global__ void __launch_bounds__(256) probe_quad(float* a) { adhip::dp_quad<1>(LA{a}, LB{a}, EPI{a}, 64, 64, 256); }
-extern "C" __global__ void __launch_bounds__(256) probe_quad_vec(float* a) { adhip::dp_quad<8>(LA{a}, LB{a}, EP4{a}, 64, 64, 4096); }
+extern "C" __global__ void __launch_bounds__(256) probe_quad(float* a) { adhip::dp_quad<1, 128>(LA{a}, LB{a}, EPI{a}, 64, 64, 256); }
+extern "C" __global__ void __launch_bounds__(256) probe_quad_vec(float* a) { adhip::dp_quad<8, 128>(LA{a}, LB{a}, EP4{a}, 64, 64, 4096); }
+extern "C" __global__ void __launch_bounds__(256) probe_quad_short(float* a) { adhip::dp_quad<1, 64>(LA{a}, LB{a}, EP4{a}, 64, 64, 64); }
 extern "C" __global__ void __launch_bounds__(256) probe_pack(float* a) { adhip::pack_bf16<0>(LA{a}, reinterpret_cast<__bf16*>(a), 64, 64, 64); }
 extern "C" __global__ void __launch_bounds__(256) probe_pack_t(float* a) { adhip::pack_bf16<1>(LB{a}, reinterpret_cast<__bf16*>(a), 64, 64, 64); }
 extern "C" __global__ void __launch_bounds__(256) probe_bf16(float* a) { adhip::dp_bf16<128, 128, 1, 64>(reinterpret_cast<const __bf16*>(a), reinterpret_cast<const __bf16*>(a), 64, EP4{a}, 64, 64); }

@@ -7,6 +7,9 @@
 //                    block tile (64..256), 4 waves, LDS-staged K panels with a
 //                    register prefetch of the next panel, optional split of K
 //                    into chunks, epilogue in registers.
+//  * dp_quad      -- the same on 32 x 32 tiles with each block's K panels
+//                    split among its 4 waves, for launches too small to
+//                    fill the device.
 //  * reduce_rows  -- Reduce+Elw, rows contiguous: waves striding over rows,
 //                    float4 or scalar coalesced loads, butterfly over the wave.
 //  * reduce_cols  -- Reduce+Elw, columns contiguous: 64 columns x 4 or 16
@@ -373,23 +376,25 @@ __device__ __forceinline__ void dp_mfma(const LA& la, const LB& lb, const EPI& e
   dp_epilogue<BM, BN>(epi, acc, smem, m0, n0, M, N, chunk);
 }
 
-// dp_quad<SPLIT>: a DotProd for launches too small to fill the device (a few
-// per-head products of 512 terms, one split weight gradient).  A 64x64 tile
-// per block leaves most compute units idle there, and each wave's chain of
-// K/2 dependent MFMAs sets the launch's time.  Here a block of 4 waves takes
-// a 32x32 output tile and splits each 128-deep K panel among its waves (wave
-// w takes panel columns 32w .. 32w+31): four times the blocks, each wave's
-// chain a quarter as long.  Panels are staged in one LDS buffer with the
+// dp_quad<SPLIT, BK>: a DotProd for launches too small to fill the device (a
+// few per-head products of 512 terms, one split weight gradient).  A 64x64
+// tile per block leaves most compute units idle there, and each wave's chain
+// of K/2 dependent MFMAs sets the launch's time.  Here a block of 4 waves
+// takes a 32x32 output tile and splits each BK-deep K panel (128, or 64 for
+// a short K) among its waves (wave w takes panel columns w*BK/4 onwards):
+// four times the blocks, each wave's chain a quarter as long.  Panels are
+// staged in one LDS buffer with the
 // next panel prefetched into registers (two barriers per panel), laid out
 // as in dp_mfma.  At the end the four 32x32 partial tiles go through LDS and
 // each thread adds its 4 consecutive elements of one row in wave order, then
 // runs the epilogue on them (float4 interface when EPI::kVec4, else per
 // element).  SPLIT > 1 splits K into chunks over blockIdx.y as in dp_mfma.
-constexpr int DPQ_BK = 128, DPQ_RPITCH = 36;
+constexpr int DPQ_RPITCH = 36;
 
-template <int SPLIT, class LA, class LB, class EPI>
+template <int SPLIT, int BK, class LA, class LB, class EPI>
 __device__ __forceinline__ void dp_quad(const LA& la, const LB& lb, const EPI& epi, int M, int N, int K) {
-  constexpr int BT = 32, BK = DPQ_BK, KW = BK / 4, H = KW / 2;
+  static_assert(BK == 64 || BK == 128, "dp_quad panels are 64 or 128 deep");
+  constexpr int BT = 32, KW = BK / 4, H = KW / 2;
   constexpr int V = BT * BK / 4 / 256;                // float4 loads per thread per operand
   constexpr bool AR = LA::kMode == 0, BR = LB::kMode == 1;
   constexpr int KP = BK + 4;

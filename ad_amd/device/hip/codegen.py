@@ -1288,22 +1288,27 @@ def _dp_epi_struct(stmts, params: Params, ity, M, N, partial_off=None, allow_vec
 # most this many terms per output ``dp_direct`` (no MFMA tile)
 SKINNY_M, DIRECT_K = 8, 8
 
-# ``dp_quad``: 32 x 32 tiles, 128-deep panels split among a block's 4 waves
-QUAD_TILE, QUAD_PANEL = 32, 128
+# ``dp_quad``: 32 x 32 tiles, K panels split among a block's 4 waves
+QUAD_TILE = 32
 # a product on 64 x 64 tiles whose K chunks have at least this many terms
 # gets a ``dp_quad`` alternative; a launch group takes it when its 64 x 64
 # blocks (all instances) number at most NARROW_MAX_BLOCKS, i.e. half the
 # compute units or fewer: there it runs four times the waves on chains a
 # quarter as long, and past that the wider tile's lower operand traffic
-# per flop wins
-QUAD_MIN_CHUNK, NARROW_MAX_BLOCKS = 256, 128
+# per flop wins (measured on the C5 step: 256 instead of 128 blocks, no
+# change; K = 64 products included or not, 63.9 steps/s either way)
+QUAD_MIN_CHUNK, NARROW_MAX_BLOCKS = 64, 128
 
 
-def quad_eligible(M, N, K, config) -> bool:
-    """A 64 x 64-tile fp32 product long enough in K for ``dp_quad``."""
+def quad_config(M, N, K, config):
+    """The ``dp_quad`` configuration of a 64 x 64-tile fp32 product long
+    enough in K (same K split; 128-deep panels, 64 for chunks shorter than
+    128 terms, so each wave still takes 16 panel columns), else None."""
     BM, BN, split, _ = config
-    return BM == 64 and BN == 64 and M > SKINNY_M and K > DIRECT_K and \
-        ceil(K / split) >= QUAD_MIN_CHUNK
+    chunk = ceil(K / split)
+    if BM == 64 and BN == 64 and M > SKINNY_M and K > DIRECT_K and chunk >= QUAD_MIN_CHUNK:
+        return QUAD_TILE, QUAD_TILE, split, 128 if chunk >= 128 else 64
+    return None
 
 
 def use_narrow(plan: "KernelPlan", instances: int) -> bool:
@@ -1344,10 +1349,10 @@ def dotprod_plan(stmts, dp, A=None, B=None, config=None, partial_off=None) -> Ke
     epi = _dp_epi_struct(stmts, params, ity, M, N, partial_off)
     init = _init_list(params)
     if BM == QUAD_TILE:
-        assert BN == QUAD_TILE and BK == QUAD_PANEL, "dp_quad takes 32 x 32 tiles and 128-deep panels"
+        assert BN == QUAD_TILE and BK in (64, 128), "dp_quad takes 32 x 32 tiles and 64- or 128-deep panels"
         src = ((la + lb + epi).replace("@FIELDS@", _fields(params)) +
                f"extern \"C\" __global__ void __launch_bounds__(256) {KNAME}({_params_decl(params)}) {{\n"
-               f"  adhip::dp_quad<{split}>(LA{{{init}}}, LB{{{init}}}, EPI{{{init}}}, {M}, {N}, {K});\n}}\n")
+               f"  adhip::dp_quad<{split}, {BK}>(LA{{{init}}}, LB{{{init}}}, EPI{{{init}}}, {M}, {N}, {K});\n}}\n")
         grid = (ceil(N / QUAD_TILE), ceil(M / QUAD_TILE) * split, 1)
         return KernelPlan(src, grid, (256, 1, 1), _plan_args(params), family="dotprod",
                           flops=2 * M * N * K)
@@ -1890,7 +1895,7 @@ def first_pass_plans(part, n, init_node, alloc: ScratchAlloc, opts=DEFAULT_OPTIO
             off = alloc.take(K * N)
             pre.append(gather_plan(B, K, N, off))
             B = _dense_scratch_operand(off, N)
-        quad = (QUAD_TILE, QUAD_TILE, cfg[2], QUAD_PANEL) if quad_eligible(M, N, K, cfg) else None
+        quad = quad_config(M, N, K, cfg)
 
         def with_narrow(main, stmts, poff=None):
             if quad is not None:

@@ -59,7 +59,8 @@ def test_dotprod_shapes(hip, M, K, N, ta, tb):
 
 @pytest.mark.parametrize("M,K,N,ta,tb,copies", [(300, 2048, 64, False, False, 1), (130, 300, 257, True, True, 1),
                                                 (512, 512, 64, False, False, 3), (96, 1000, 100, False, True, 1),
-                                                (64, 260, 36, True, False, 2), (512, 512, 64, True, True, 16)])
+                                                (64, 260, 36, True, False, 2),
+                                                (512, 64, 512, False, True, 1), (130, 70, 257, True, False, 1), (512, 512, 64, True, True, 16)])
 def test_narrow_launch_parity(hip, M, K, N, ta, tb, copies):
     """Launch groups too small to fill the device run ``dp_quad`` (32 x 32
     tiles, each block's K panels split among its four waves, partial tiles

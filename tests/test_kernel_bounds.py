@@ -156,7 +156,8 @@ def test_single_buffer_tiles_stay_in_bounds(workdir, M, K, N, ta, tile):
 
 @pytest.mark.parametrize("M,K,N,ta,tb,copies", [(300, 2048, 64, False, False, 1), (130, 300, 257, True, True, 1),
                                                 (512, 512, 64, False, False, 3), (96, 1000, 100, False, True, 1),
-                                                (64, 260, 36, True, False, 2)])
+                                                (64, 260, 36, True, False, 2),
+                                                (512, 64, 512, False, True, 1), (130, 70, 257, True, False, 1)])
 def test_narrow_launches_stay_in_bounds(workdir, M, K, N, ta, tb, copies):
     """Launch groups too small to fill the device run ``dp_quad`` (32 x 32
     tiles, 128-deep panels split among the waves): ragged M, N and K, K
@@ -175,7 +176,7 @@ def test_narrow_launches_stay_in_bounds(workdir, M, K, N, ta, tb, copies):
     ok, log = check_run(ad.compile_proc(), workdir)
     assert ok, log
     text = "".join(open(f).read() for f in _sources(workdir))
-    assert re.search(r"dp_quad<\d+>", text) and not re.search(r"dp_mfma<64, 64,", text)
+    assert re.search(r"dp_quad<\d+, (64|128)>", text) and not re.search(r"dp_mfma<64, 64,", text)
 
 
 def test_streamed_accesses_stay_in_bounds(workdir):
