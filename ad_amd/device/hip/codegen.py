@@ -564,8 +564,9 @@ class _StoreTracker:
     """The regions one element has stored to so far, and the operand reads
     hoisted ahead of every store (``_l[k]``, up to ``limit`` of them)."""
 
-    def __init__(self, limit):
+    def __init__(self, limit, slot="_l[{}]"):
         self.limit = limit
+        self.slot = slot                # how a hoisted read is named (its index filled in)
         self.stored: List[tuple] = []
         self.scratch_stored = False
         self.loads: List[str] = []
@@ -592,7 +593,7 @@ class _StoreTracker:
                 return None
             self._idx[expr] = len(self.loads)
             self.loads.append(expr)
-        return f"_l[{self._idx[expr]}]"
+        return self.slot.format(self._idx[expr])
 
     def note(self, km):
         if getattr(km, "scratch_offset", None) is not None:
@@ -806,6 +807,36 @@ class Lowerer:
             self._note_store(n.kres)
         return lines
 
+    def prefetched_statements(self, stmts, init_value, batch) -> List[str]:
+        """``statements`` with every operand read that no earlier store of
+        the element can reach issued ahead of the statements, ``batch``
+        distinct reads at a time: a batch's reads (``_pK``), a scheduling
+        barrier, then the statements up to the one that completed the
+        batch.  Without the barrier the compiler may keep the loads next to
+        their uses and wait for each in turn (a pass of 58 scaled copies
+        compiled to 116 loads, each followed by a wait for all memory
+        operations).  A read is hoisted only past stores that cannot reach
+        it (``_StoreTracker.free``); a concat read moves whole, condition
+        included."""
+        self.hoist = True
+        self.stores = _StoreTracker(1 << 30, slot="_p{}")
+        out, body, first = [], [], 0
+
+        def flush():
+            nonlocal body, first
+            new = self.stores.loads[first:]
+            out.extend(f"const float _p{first + i} = {e};" for i, e in enumerate(new))
+            if new:
+                out.append("__builtin_amdgcn_sched_barrier(0);")
+            out.extend(body)
+            body, first = [], len(self.stores.loads)
+        for st in stmts:
+            body.extend(self.statements([st], init_value))
+            if len(self.stores.loads) - first >= batch:
+                flush()
+        flush()
+        return out
+
 
 def _ity(bound) -> str:
     return "unsigned" if bound < (1 << 31) else "unsigned long long"
@@ -921,6 +952,11 @@ def _distinct_loads(stmts) -> int:
     return len(seen)
 
 
+# operand reads issued together ahead of the statements of a heavy
+# one-element-per-thread pass (``Lowerer.prefetched_statements``)
+PREFETCH_BATCH = 64
+
+
 def elementwise_plan(stmts, n, index_kind="global", n_cols=1, flops=0, init_value=None) -> KernelPlan:
     """One thread per element (or per 4 elements when every access allows a
     float4), statements in order.  ``index_kind`` defines ``_x``/``_y`` for
@@ -944,7 +980,9 @@ def elementwise_plan(stmts, n, index_kind="global", n_cols=1, flops=0, init_valu
         # elements: 141 -> 125 us)
         low = Lowerer(ity, params, stream=heavy and n > SCALAR_MAX_N and
                       4 * n * _distinct_loads(stmts) > STREAM_PASS_BYTES)
-        body = "\n    ".join(low.statements(stmts, init_value))
+        lines = low.prefetched_statements(stmts, init_value, PREFETCH_BATCH) if heavy else \
+            low.statements(stmts, init_value)
+        body = "\n    ".join(lines)
         src = f"""extern "C" __global__ void __launch_bounds__({block}) {KNAME}({_params_decl(params)}{', ' if params.slots else ''}unsigned long long n_) {{
   const {ity} _global_id = ({ity})blockIdx.x * {block}u + threadIdx.x;
   if (_global_id >= ({ity})n_) return;

@@ -48,6 +48,7 @@ template <class T> static inline T __shfl_xor(T v, int, int = 64) { return v; }
 #define __builtin_amdgcn_fence(...) ((void)0)
 #define __builtin_amdgcn_iglp_opt(...) ((void)0)
 #define __builtin_amdgcn_s_setprio(...) ((void)0)
+#define __builtin_amdgcn_sched_barrier(...) ((void)0)
 #define __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, ...) (c)
 #define __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, ...) (c)
 using std::exp2; using std::log2; using std::sin; using std::sqrt; using std::fabs;

@@ -562,6 +562,41 @@ def test_short_heavy_pass_matches_oracle(hip):
     np.testing.assert_allclose(a["y"], b["y"], rtol=1e-5, atol=1e-6)
 
 
+def test_heavy_pass_prefetch_batches_match_oracle(hip):
+    """A 2^16-element pass reading 70 inputs (more than one prefetch batch
+    of operand reads), a concat operand, the same input read by several
+    statements, and partial results stored and read back by later
+    statements of the same pass: the reads issued ahead in batches give the
+    oracle's values."""
+    from ad_amd.device.hip import codegen
+
+    def build():
+        rng = np.random.default_rng(8)
+        xs = [Tensor(rng.standard_normal((256, 256)).astype(np.float32)) for _ in range(70)]
+        c = ad.concat([xs[0][:128] * 2.0, xs[1][128:] * 3.0], 0)
+        y = c * xs[2]
+        parts = []
+        for i, x in enumerate(xs[3:]):
+            y = y * 0.5 + x * xs[i % 7]
+            if i in (20, 45, 66):
+                parts.append(y * 1.5)
+        got = {}
+        Receiver(lambda *v: got.update(v=[a.copy() for a in v]), parts)
+        return got
+    ad.reset()
+    a = build()
+    dev = hip()
+    ad.execute(device=dev)
+    srcs = [p.source for ps in dev.kernels.values() for p in ps]
+    assert any(src.count("__builtin_amdgcn_sched_barrier(0)") >= 2 for src in srcs), "no batched pass"
+    ad.reset()
+    b = build()
+    ad.execute(device=OracleDevice())
+    for x, y in zip(a["v"], b["v"]):
+        np.testing.assert_allclose(x, y, rtol=1e-5, atol=1e-6)
+    assert codegen.PREFETCH_BATCH < 70
+
+
 def test_wide_sum_of_many_operands_matches_oracle(hip):
     """A 2^20-element sum of 20 inputs with a broadcast row factor and two
     stored partial sums (one element per thread, many operands)."""
