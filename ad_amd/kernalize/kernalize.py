@@ -135,6 +135,6 @@ def calc_exprs(node, _):
 
 
 def kernalize(context):
-    for idx in range(len(context.procedure)):
-        context.procedure[idx].nodes = walk_graph(context.procedure[idx].nodes, fill_child_datacmds)
-        context.procedure[idx].nodes = walk_graph(context.procedure[idx].nodes, calc_exprs)
+    for block in context.procedure:
+        for visit in (fill_child_datacmds, calc_exprs):
+            block.nodes = walk_graph(block.nodes, visit)

@@ -289,11 +289,10 @@ def linearize(main_block: Block) -> Proc:
     global global_deps, id_to_node, block_to_node
     id_to_node = {}
 
-    def insert_id_to_node(node, _):
-        if node.id not in id_to_node:
-            id_to_node[node.id] = node
+    def record(node, _):
+        id_to_node.setdefault(node.id, node)     # the first node seen under an id
         return node
-    walk_graph(main_block, insert_id_to_node, walk_block=True, walk_child=True)
+    walk_graph(main_block, record, walk_block=True, walk_child=True)
 
     global_deps = {}
     block_to_node = {}
