@@ -38,6 +38,18 @@ def _ranges_intersect(r1, r2) -> bool:
     return r1[0] < r2[1] and r2[0] < r1[1]
 
 
+def _groups_by_sweep(lo, hi):
+    """Merged groups of ranges sorted by start, with the pairwise test of
+    the reference loop (it matters for empty ranges)."""
+    out = []
+    for a, b in zip(lo.tolist(), hi.tolist()):
+        if out and a < out[-1][1] and out[-1][0] < b:
+            out[-1] = (min(out[-1][0], a), max(out[-1][1], b))
+        else:
+            out.append((a, b))
+    return np.array([g[0] for g in out], dtype=np.int64), np.array([g[1] for g in out], dtype=np.int64)
+
+
 def place(entries: List[VarEntry]) -> int:
     """Assign ``offset`` to each entry (already sorted largest first);
     return the arena high-water mark.
@@ -45,8 +57,11 @@ def place(entries: List[VarEntry]) -> int:
     For each entry: the ranges of already placed entries whose lifetimes
     overlap it, stably sorted by start, intersecting neighbours merged; the
     entry goes into the last gap between consecutive ranges that is wide
-    enough, else at the end of the last range, else at 0.  The lifetime
-    query runs vectorised over all placed entries."""
+    enough, else at the end of the last range, else at 0.  Everything runs
+    vectorised over the placed entries: when every range is non-empty, a
+    sorted range starts a new merged group exactly when it starts at or
+    after the largest end before it, and a group ends at the largest end
+    within it (empty ranges take the reference's pairwise sweep)."""
     n = len(entries)
     starts = np.fromiter((e.start_idx for e in entries), dtype=np.int64, count=n)
     ends = np.fromiter((e.end_idx for e in entries), dtype=np.int64, count=n)
@@ -55,24 +70,21 @@ def place(entries: List[VarEntry]) -> int:
     high = 0
     for i, entry in enumerate(entries):
         live = np.nonzero(np.maximum(starts[:i], starts[i]) < np.minimum(ends[:i], ends[i]))[0]
-        lo = offsets[live]
-        order = np.argsort(lo, kind="stable")     # Python's stable sort by start
-        taken = list(zip(lo[order].tolist(), (lo[order] + sizes[live][order]).tolist()))
-        j = 0
-        while j < len(taken) - 1:
-            if _ranges_intersect(taken[j], taken[j + 1]):
-                merged = (min(taken[j][0], taken[j + 1][0]), max(taken[j][1], taken[j + 1][1]))
-                del taken[j]
-                del taken[j]
-                taken.insert(j, merged)
+        if len(live) == 0:
+            offset = 0
+        else:
+            order = np.argsort(offsets[live], kind="stable")     # Python's stable sort by start
+            lo = offsets[live][order]
+            sz = sizes[live][order]
+            if sz.min() > 0:
+                reach = np.maximum.accumulate(lo + sz)
+                first = np.flatnonzero(lo[1:] >= reach[:-1]) + 1      # ranges that start a group
+                group_lo = np.concatenate(([lo[0]], lo[first]))
+                group_hi = reach[np.append(first - 1, len(lo) - 1)]
             else:
-                j += 1
-        offset = -1
-        for t in range(len(taken) - 1):
-            if taken[t + 1][0] - taken[t][1] >= entry.size:
-                offset = taken[t][1]
-        if offset == -1:
-            offset = taken[-1][-1] if len(taken) > 0 else 0
+                group_lo, group_hi = _groups_by_sweep(lo, lo + sz)
+            wide = np.flatnonzero(group_lo[1:] - group_hi[:-1] >= entry.size)
+            offset = int(group_hi[wide[-1]]) if len(wide) else int(group_hi[-1])
         entry.offset = offset
         offsets[i] = offset
         high = max(high, offset + entry.size)

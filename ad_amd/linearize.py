@@ -64,10 +64,11 @@ def get_deps_global(block: Block, outer: Dict[int, int] = None):
     outer = {} if outer is None else outer
     defined: Dict[int, int] = {}
     needs: Dict[int, int] = {}
+    finished = set()
     for node in block.nodes:
         body = node.get_block()
         if body is None:
-            _collect(node, block, outer, defined, needs)
+            _collect(node, block, outer, defined, needs, finished)
             continue
         body_defined, body_needs = get_deps_global(body, outer | defined)
         for dep, where in list(body_needs.items()):
@@ -80,16 +81,20 @@ def get_deps_global(block: Block, outer: Dict[int, int] = None):
     return defined, needs
 
 
-def _collect(root, block, outer, defined, needs):
+def _collect(root, block, outer, defined, needs, finished):
     """Depth-first from ``root`` through the ids each node reads, recording
     waits.  A node's reads are visited in order, each one's subtree before
     the next read; a node is marked defined after its reads (post-order).
     Nodes of outer blocks, or already entered from this root, are not
-    entered again; ids defined in another loop body stand for that loop."""
+    entered again; ids defined in another loop body stand for that loop.
+    A node whose walk already finished (from an earlier root of the block)
+    is not entered again either: its walk would record the same waits into
+    the same sets and define nothing new."""
     entered = set()
 
     def enterable(node):
-        return isinstance(node, Node) and node.id not in entered and node.id not in outer
+        return isinstance(node, Node) and node.id not in entered and node.id not in outer \
+            and node.id not in finished
 
     if not enterable(root):
         return
@@ -98,6 +103,7 @@ def _collect(root, block, outer, defined, needs):
         node, reads, cursor = stack[-1]
         if cursor[0] == len(reads):
             stack.pop()
+            finished.add(node.id)
             if node.id not in defined:
                 defined[node.id] = block.id
             continue

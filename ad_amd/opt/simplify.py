@@ -21,6 +21,7 @@ is_new = False
 def reset_state():
     global is_new
     is_new = False
+    _settled.clear()
 
 
 def _is_const(n, value=None):
@@ -79,37 +80,65 @@ def _rewrite(node):
     return None
 
 
-def _visit_operands(node, visited):
+def _operand_names(node):
     if hasattr(node, "left") and hasattr(node, "right"):
-        node.left = _inner_simpl(node.left, visited, on_child=True)
-        node.right = _inner_simpl(node.right, visited, on_child=True)
-        return True
+        return ("left", "right")
     if hasattr(node, "child"):
-        node.child = _inner_simpl(node.child, visited, on_child=True)
-        return True
-    return False
+        return ("child",)
+    return ()
+
+
+def _visit_operands(node, visited):
+    """Simplify the operands in order; (whether ``node`` has operands,
+    whether any operand was replaced)."""
+    names = _operand_names(node)
+    changed = False
+    for name in names:
+        old = getattr(node, name)
+        new = _inner_simpl(old, visited, on_child=True)
+        setattr(node, name, new)
+        changed |= new is not old
+    return bool(names), changed
+
+
+# ids of nodes already at their fixpoint within the current simpl_node walk:
+# no rule fired on the node, none of its operands was replaced while it was
+# visited, and every operand is itself in the set.  Nothing beneath such a
+# node can change any more, so re-walks skip it (the repeated walk of a
+# top-level node's operands after each rewrite was most of the pass's time)
+_settled = set()
 
 
 def _inner_simpl(node, visited, on_child=False):
     global is_new
     if node.id in visited:
         return node
+    if node.id in _settled:
+        if not on_child:
+            is_new = False
+        visited[node.id] = 1
+        return node
     replacement = _rewrite(node)
     if replacement is not None:
         return replacement
     if not on_child:
         is_new = False
-    _visit_operands(node, visited)
+    has_operands, changed = _visit_operands(node, visited)
     if not on_child:
         while is_new:
             visited = {}
             is_new = False
-            if not _visit_operands(node, visited):
+            has_operands, again = _visit_operands(node, visited)
+            changed |= again
+            if not has_operands:
                 break
     visited[node.id] = 1
+    if not changed and all(getattr(node, name).id in _settled for name in _operand_names(node)):
+        _settled.add(node.id)
     return node
 
 
 def simpl_node(context):
+    _settled.clear()
     context.procedure[0] = walk_graph(context.procedure[0], _inner_simpl,
                                       walk_block=True, walk_child=True)

@@ -341,6 +341,23 @@ def test_tetris_place_matches_direct_loop(seed):
     assert [e.offset for e in a] == [e.offset for e in b]
 
 
+@pytest.mark.parametrize("seed", range(10))
+def test_tetris_place_matches_direct_loop_positive_sizes(seed):
+    """Only non-empty ranges: every query takes the vectorised merge."""
+    import copy
+    import random
+    from ad_amd.alloc.tetris_opt import VarEntry, place, place_reference
+    rng = random.Random(100 + seed)
+    entries = []
+    for v in range(rng.randint(200, 600)):
+        s0 = rng.randint(0, 300)
+        entries.append(VarEntry(v, s0, s0 + rng.randint(1, 60), rng.choice([1, 2, 4, 8, 64, rng.randint(1, 500)])))
+    entries.sort(key=lambda e: -e.size)
+    a, b = copy.deepcopy(entries), copy.deepcopy(entries)
+    assert place(a) == place_reference(b)
+    assert [e.offset for e in a] == [e.offset for e in b]
+
+
 @pytest.mark.parametrize("build", ["mlp", "layernorm", "transformer", "batched"])
 def test_lazy_white_list_matches_walking_paths(build):
     """The whole compiled Proc (command order, fused groups, access
