@@ -30,6 +30,17 @@ class ChildrenType(Enum):
     RECEIVER = 3
 
 
+_CONTEXT_TYPES = []
+
+
+def _context_types():
+    """(Block, Proc), imported on first use (the context module imports this one)."""
+    if not _CONTEXT_TYPES:
+        from .context import Block, Proc
+        _CONTEXT_TYPES.extend((Block, Proc))
+    return _CONTEXT_TYPES
+
+
 class Node:
     """A traced value.  Operands are held as ``child`` (one), ``left`` /
     ``right`` (two) or ``rec_children`` (a Receiver's list); once kernalized,
@@ -116,14 +127,12 @@ class Node:
         return self.id == other.id
 
     def get_block(self):
-        from .context import Block
         block = getattr(self, "block", None)
-        return block if isinstance(block, Block) else None
+        return block if block is not None and isinstance(block, _context_types()[0]) else None
 
     def get_proc(self):
-        from .context import Proc
         proc = getattr(self, "proc", None)
-        return proc if isinstance(proc, Proc) else None
+        return proc if proc is not None and isinstance(proc, _context_types()[1]) else None
 
     def rename(self, fr: int, to: int):
         for k in self.kargs:
