@@ -814,8 +814,8 @@ class Lowerer:
         barrier, then the statements up to the one that completed the
         batch.  Without the barrier the compiler may keep the loads next to
         their uses and wait for each in turn (a pass of 58 scaled copies
-        compiled to 116 loads, each followed by a wait for all memory
-        operations).  A read is hoisted only past stores that cannot reach
+        compiled to 174 loads, 167 of them followed by a wait for all
+        memory operations).  A read is hoisted only past stores that cannot reach
         it (``_StoreTracker.free``); a concat read moves whole, condition
         included."""
         self.hoist = True

@@ -529,7 +529,7 @@ class HIPDevice(Device):
                     members = [launches[i] for i in group]
                     plan = members[0].plan
                     # a group too small to fill the device takes the plans'
-                    # dp_quad alternative (same arguments, same results)
+                    # dp_quad alternative (same arguments and results layout)
                     narrow = self.narrow_launches and codegen.use_narrow(plan, len(members))
                     if narrow:
                         plan = plan.narrow
