@@ -877,6 +877,8 @@ def _moving(index_kind):
     group of 4 elements, and those that are 0, per element space."""
     if index_kind == "dp":
         return (Global, Y), ()            # valid when the row length is a multiple of 4
+    if index_kind == "dpT":
+        return (Global, X), ()            # valid when the column length is a multiple of 4
     if index_kind == "red":
         return (Global, X), (Y,)
     return (Global,), ()
@@ -906,7 +908,7 @@ def _vector_plan(stmts, n, index_kind="global", n_cols=1):
     and 4-aligned, or constant over aligned groups of 4 (a concat's condition
     too), and every write contiguous and aligned, with folded offsets that
     are multiples of 4 floats."""
-    if n % 4 != 0 or (index_kind == "dp" and n_cols % 4 != 0):
+    if n % 4 != 0 or (index_kind in ("dp", "dpT") and n_cols % 4 != 0):
         return False
     for kind, node in stmts:
         if kind in ("tmp", "load", "store", "sum"):
@@ -926,6 +928,9 @@ def _index_setup(index_kind, ity, n_cols):
     if index_kind == "dp":
         return (f"const {ity} _x = _global_id / ({ity}){n_cols}; "
                 f"const {ity} _y = _global_id % ({ity}){n_cols}; (void)_x; (void)_y;")
+    if index_kind == "dpT":                 # elements in column order; n_cols = rows
+        return (f"const {ity} _x = _global_id % ({ity}){n_cols}; "
+                f"const {ity} _y = _global_id / ({ity}){n_cols}; (void)_x; (void)_y;")
     if index_kind == "red":
         return f"const {ity} _x = _global_id; const {ity} _y = 0; (void)_x; (void)_y;"
     return ""
@@ -1865,15 +1870,38 @@ class _Stmt:
 GATHER_MIN_MACS = 1 << 22
 
 
-def gather_plan(karg, rows, cols, dst_off) -> KernelPlan:
-    """Dense row-major copy ``scratch[r * cols + c] = operand(r, c)`` of a
-    DotProd operand in the (_x, _y) convention of its kernel arg."""
+def gather_plan(karg, rows, cols, dst_off, column_major=False) -> KernelPlan:
+    """Dense copy of a DotProd operand in the (_x, _y) convention of its
+    kernel arg: row-major ``scratch[r * cols + c] = operand(r, c)``, or
+    column-major ``scratch[c * rows + r]`` with threads along the rows."""
     sink = _scratch_km(dst_off, Global())
+    if column_major:
+        return elementwise_plan([("copy", _Stmt([karg], sink))], rows * cols, index_kind="dpT", n_cols=rows)
     return elementwise_plan([("copy", _Stmt([karg], sink))], rows * cols, index_kind="dp", n_cols=cols)
 
 
-def _dense_scratch_operand(off, cols):
+def _dense_scratch_operand(off, cols, rows=None):
+    """The gathered copy as an operand: row-major, or column-major when
+    ``rows`` is given."""
+    if rows is not None:
+        return _scratch_km(off, Add(Mult(Y(), Val(Constant(rows))), X()))
     return _scratch_km(off, Add(Mult(X(), Val(Constant(cols))), Y()))
+
+
+def _runs_along_rows(karg) -> bool:
+    """Every piece of a concat operand is contiguous along its row index
+    (_x) and not along its column index (_y): a row-major gather would read
+    each piece across its storage, a column-major one reads it in order."""
+    leaves = [km for km in _iter_kmatrix(karg)]
+    if not leaves:
+        return False
+    for km in leaves:
+        if km.is_temp:
+            return False
+        core, _ = split_const(km.access)
+        if vec_class(core, X).kind != AFF or vec_class(core, Y).kind == AFF:
+            return False
+    return True
 
 
 # a DotProd epilogue reading more distinct buffer locations than this runs as
@@ -1927,12 +1955,14 @@ def first_pass_plans(part, n, init_node, alloc: ScratchAlloc, opts=DEFAULT_OPTIO
         pre = []
         if isinstance(A, KConcat) and M * N * K >= GATHER_MIN_MACS:
             off = alloc.take(M * K)
-            pre.append(gather_plan(A, M, K, off))
-            A = _dense_scratch_operand(off, K)
+            by_col = _runs_along_rows(A)
+            pre.append(gather_plan(A, M, K, off, by_col))
+            A = _dense_scratch_operand(off, K, M if by_col else None)
         if isinstance(B, KConcat) and M * N * K >= GATHER_MIN_MACS:
             off = alloc.take(K * N)
-            pre.append(gather_plan(B, K, N, off))
-            B = _dense_scratch_operand(off, N)
+            by_col = _runs_along_rows(B)
+            pre.append(gather_plan(B, K, N, off, by_col))
+            B = _dense_scratch_operand(off, N, K if by_col else None)
         quad = quad_config(M, N, K, cfg)
 
         def with_narrow(main, stmts, poff=None):

@@ -266,6 +266,36 @@ def test_dotprod_concat_operands(hip):
     np.testing.assert_allclose(got["r"], a @ b, rtol=0, atol=bound)
 
 
+@pytest.mark.parametrize("ragged", [False, True])
+def test_dotprod_concat_of_transposed_pieces(hip, ragged):
+    """Operands whose concat pieces run along the product's rows (transposed
+    pieces, concatenated along K for A and along K for B) are gathered
+    column-major, reading every piece in order; the product reads the copy
+    along its contiguous axis.  Ragged: piece widths and M not multiples of
+    4 (a scalar gather)."""
+    from ad_amd.device.hip import codegen
+    rng = np.random.default_rng(11 + ragged)
+    M, N = (257, 130) if ragged else (256, 128)
+    ka = [61, 67, 128] if ragged else [64, 64, 128]
+    pa = [rng.standard_normal((k, M)).astype(np.float32) for k in ka]        # piece^T is [M, k]
+    pb = [rng.standard_normal((N, k)).astype(np.float32) for k in ka]        # piece^T is [k, N]
+    A = ad.concat([Tensor(x).T() for x in pa], 1)
+    B = ad.concat([Tensor(x).T() for x in pb], 0)
+    K = sum(ka)
+    assert M * N * K >= codegen.GATHER_MIN_MACS
+    r = A @ B
+    got = {}
+    Receiver(lambda v: got.setdefault("r", v.copy()), [r])
+    dev = hip()
+    ad.execute(device=dev)
+    srcs = [p.source for ps in dev.kernels.values() for p in ps]
+    assert sum("_x = _global_id % " in src for src in srcs) == 2, "both operands gathered column-major"
+    a = np.concatenate([x.T for x in pa], 1).astype(np.float64)
+    b = np.concatenate([x.T for x in pb], 0).astype(np.float64)
+    bound = np.sqrt(K) * np.finfo(np.float32).eps * (np.abs(a) @ np.abs(b))
+    assert np.all(np.abs(got["r"] - a @ b) <= bound)
+
+
 @pytest.mark.parametrize("rows,cols", [(4096, 256), (16384, 64), (1000, 100)])
 def test_column_reduce_split(hip, rows, cols):
     """Reductions over rows of a row-major matrix (bias / LayerNorm gradient

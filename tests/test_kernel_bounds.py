@@ -213,3 +213,21 @@ def test_wide_streamed_pass_stays_in_bounds(workdir, monkeypatch):
 
 def _sources(workdir):
     return [os.path.join(workdir, f) for f in os.listdir(workdir) if f.endswith(".cpp")]
+
+
+@pytest.mark.parametrize("ragged", [False, True])
+def test_column_major_gathers_stay_in_bounds(workdir, ragged):
+    """Concat operands whose pieces run along the product's rows are
+    gathered column-major (threads along the rows, float4 where aligned)."""
+    import numpy as np
+    from ad_amd.graph import Receiver, Tensor
+    rng = np.random.default_rng(11 + ragged)
+    M, N = (257, 130) if ragged else (256, 128)
+    ka = [61, 67, 128] if ragged else [64, 64, 128]
+    A = ad.concat([Tensor(rng.standard_normal((k, M)).astype(np.float32)).T() for k in ka], 1)
+    B = ad.concat([Tensor(rng.standard_normal((N, k)).astype(np.float32)).T() for k in ka], 0)
+    Receiver(lambda v: None, [(A @ B).sigmoid()])
+    ok, log = check_run(ad.compile_proc(), workdir)
+    assert ok, log
+    text = "".join(open(f).read() for f in _sources(workdir))
+    assert text.count("_x = _global_id % ") >= 2
