@@ -77,6 +77,7 @@ class RecordingContext:
         self.base = FAKE_BASE
         self.h = 1
         self.writes, self.launches, self.errors = [], [], []
+        self.reads = []                # (arena offset, bytes) of every host read, in order
         self._capture = None           # launches of the graph being captured
         self._graphs = {}
         self._staging = {}             # tag -> open
@@ -101,6 +102,7 @@ class RecordingContext:
 
     def read(self, off, out):
         self._check(off, out.nbytes, "read")
+        self.reads.append((off, out.nbytes))
 
     def copy(self, dst, src, n):
         self._check(dst, n, "copy to")
@@ -266,16 +268,18 @@ def _host_source(src):
     return re.sub(r"__attribute__\(\(address_space\(\d\)\)\)", "", src)
 
 
-def check_run(proc, workdir, shrink=None, device=None, **device_options):
+def check_run(proc, workdir, shrink=None, device=None, dump=None, **device_options):
     """Run ``proc`` through a recording HIPDevice (loops replayed as
     recorded graphs), then check transfers and argument tables
     (``check_tables``) and run every launch on the host under
     AddressSanitizer.  ``device`` reuses a recording device (a second
     program on one device); ``shrink`` (bytes) cuts the host arena short, to
-    show the check catches an access past it.  Returns ``(ok, log)``."""
+    show the check catches an access past it; ``dump`` (a path) receives the
+    arena after the last launch.  Returns ``(ok, log)``."""
     dev = device or recording_device(**device_options)
     mark = len(dev.ctx.launches)
     dev.ctx.writes = []
+    dev.ctx.reads = []
     dev.execute(proc)
     ctx = dev.ctx
     sources = dev.recorded_sources
@@ -324,6 +328,8 @@ def check_run(proc, workdir, shrink=None, device=None, **device_options):
         seen.add((func, grid, row))
         text.append(f'  fprintf(stderr, "launch {k} {func}\\n"); adhip_launch({func}, '
                     f"(const unsigned long long*)(a + {row - FAKE_BASE}ull), {grid[0]}, {grid[1]}, {grid[2]}, {block[0]});")
+    if dump:
+        text.append(f'  {{ FILE* out = fopen("{dump}", "wb"); if (!out || fwrite(a, 1, n, out) != n) return 4; fclose(out); }}')
     text.append('  fprintf(stderr, "all launches in bounds\\n");\n  return 0;\n}')
     code = "\n".join(text)
     exe = os.path.join(workdir, "run_" + hashlib.sha1(code.encode()).hexdigest()[:12])
@@ -336,3 +342,20 @@ def check_run(proc, workdir, shrink=None, device=None, **device_options):
     env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0")
     r = subprocess.run([exe], capture_output=True, text=True, timeout=600, env=env)
     return r.returncode == 0 and "all launches in bounds" in r.stderr, r.stderr[-4000:]
+
+
+def host_values(proc, workdir, **device_options):
+    """Values of every host read (Receiver) of a Proc computed by running its
+    launches on the host, in read order; None if a launch leaves the arena.
+    Only kernels whose lanes do not exchange data (elementwise passes,
+    operand gathers, copies) compute real values here: cross-lane and MFMA
+    builtins return their inputs and a block's threads run one after
+    another.  Each distinct launch runs once, so a Proc with loops gives
+    the values of one pass through each body."""
+    dump = os.path.join(workdir, "arena_after.bin")
+    dev = recording_device(**device_options)
+    ok, log = check_run(proc, workdir, device=dev, dump=dump)
+    if not ok:
+        return None
+    arena = np.fromfile(dump, dtype=np.uint8)
+    return [arena[off:off + nb].view(np.float32).copy() for off, nb in dev.ctx.reads]

@@ -1,0 +1,84 @@
+"""Values of elementwise passes computed on the host (``host_values``: the
+device's own kernels run on the CPU over its arena) against the CPU oracle.
+
+Elementwise kernels exchange no data between lanes, so the host run computes
+their real results.  This checks the generated statement code itself on the
+CPU -- including heavy passes (more statements than
+``codegen.SCALAR_MIN_STMTS`` over at most ``SCALAR_MAX_N`` elements), whose
+operand reads are issued in batches ahead of the statements -- before any
+GPU run."""
+import numpy as np
+import pytest
+
+import ad_amd as ad
+from ad_amd.graph import Receiver, Tensor
+from oracle import OracleDevice
+
+from .host_emulation import host_values, recording_device
+
+
+def _chain(seed, n_inputs, n_ops, shape, tweak=None):
+    """A chain of elementwise statements over ``n_inputs`` tensors with a
+    concat operand, two received intermediate values and the same inputs
+    read by many statements; ``tweak`` changes one constant (statement
+    ``tweak``)."""
+    rng = np.random.default_rng(seed)
+    xs = [Tensor(rng.uniform(0.5, 1.5, shape).astype(np.float32)) for _ in range(n_inputs)]
+    half = shape[0] // 2
+    y = ad.concat([xs[0][:half] * 2.0, xs[1][half:] * 0.5], 0)
+    outs = []
+    for i in range(n_ops):
+        x = xs[int(rng.integers(0, n_inputs))]
+        kind = int(rng.integers(0, 5))
+        c = 0.75 if i != tweak else 0.7501
+        if kind == 0:
+            y = y * c + x
+        elif kind == 1:
+            y = (y * x).sqrt() + 0.25 * c
+        elif kind == 2:
+            y = y * c + x * xs[i % n_inputs]
+        elif kind == 3:
+            y = (y * 0.125 * c).exp2() * x
+        else:
+            y = y * c + (x - 1.0).sin()
+        if i in (n_ops // 3, (2 * n_ops) // 3):
+            outs.append(y * 1.0)
+    outs.append(y)
+    got = {}
+    Receiver(lambda *v: got.update(v=[a.copy() for a in v]), outs)
+    return got
+
+
+def _host_and_oracle(tmp_path, seed, n_inputs, n_ops, shape, tweak=None):
+    ad.reset()
+    _chain(seed, n_inputs, n_ops, shape, tweak)
+    proc = ad.compile_proc()
+    probe = recording_device()
+    probe.prepare(proc)
+    heavy = sum(p.source.count("__builtin_amdgcn_sched_barrier(0)") for ps in probe.kernels.values() for p in ps)
+    ad.reset()
+    _chain(seed, n_inputs, n_ops, shape, tweak)
+    vals = host_values(ad.compile_proc(), str(tmp_path))
+    ad.reset()
+    ref = _chain(seed, n_inputs, n_ops, shape)
+    ad.execute(device=OracleDevice())
+    return heavy, vals, ref["v"]
+
+
+@pytest.mark.parametrize("seed,n_inputs,n_ops", [(0, 8, 12), (1, 40, 20), (2, 80, 30)])
+def test_heavy_pass_values_on_host_match_oracle(tmp_path, seed, n_inputs, n_ops):
+    """Heavy passes of one batch and of several (up to 80 inputs plus the
+    concat pieces: more reads than one batch of 64)."""
+    heavy, vals, ref = _host_and_oracle(tmp_path, seed, n_inputs, n_ops, (128, 128))
+    assert heavy >= 1 + (n_inputs > 64), "the program has no (multi-batch) heavy pass"
+    assert vals is not None, "a launch left the arena"
+    for got, want in zip(vals, ref):
+        np.testing.assert_allclose(got.reshape(want.shape), want, rtol=1e-6, atol=1e-6)
+
+
+def test_host_values_see_a_changed_constant(tmp_path):
+    """The check has teeth: the same program with one constant changed
+    gives values the oracle's run of the original does not."""
+    heavy, vals, ref = _host_and_oracle(tmp_path, 1, 40, 20, (128, 128), tweak=15)
+    assert heavy >= 1 and vals is not None
+    assert not np.allclose(vals[-1].reshape(ref[-1].shape), ref[-1], rtol=1e-6, atol=1e-6)
