@@ -344,6 +344,16 @@ def check_run(proc, workdir, shrink=None, device=None, dump=None, **device_optio
     return r.returncode == 0 and "all launches in bounds" in r.stderr, r.stderr[-4000:]
 
 
+def host_arena(proc, workdir, **device_options):
+    """Run ``proc``'s launches on the host (``check_run``) and return the
+    recording device and the arena bytes after the last launch (None if a
+    launch leaves the arena)."""
+    dump = os.path.join(workdir, "arena_after.bin")
+    dev = recording_device(**device_options)
+    ok, log = check_run(proc, workdir, device=dev, dump=dump)
+    return dev, (np.fromfile(dump, dtype=np.uint8) if ok else None)
+
+
 def host_values(proc, workdir, **device_options):
     """Values of every host read (Receiver) of a Proc computed by running its
     launches on the host, in read order; None if a launch leaves the arena.
@@ -352,10 +362,7 @@ def host_values(proc, workdir, **device_options):
     builtins return their inputs and a block's threads run one after
     another.  Each distinct launch runs once, so a Proc with loops gives
     the values of one pass through each body."""
-    dump = os.path.join(workdir, "arena_after.bin")
-    dev = recording_device(**device_options)
-    ok, log = check_run(proc, workdir, device=dev, dump=dump)
-    if not ok:
+    dev, arena = host_arena(proc, workdir, **device_options)
+    if arena is None:
         return None
-    arena = np.fromfile(dump, dtype=np.uint8)
     return [arena[off:off + nb].view(np.float32).copy() for off, nb in dev.ctx.reads]

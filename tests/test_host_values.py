@@ -14,7 +14,7 @@ import ad_amd as ad
 from ad_amd.graph import Receiver, Tensor
 from oracle import OracleDevice
 
-from .host_emulation import host_values, recording_device
+from .host_emulation import host_arena, host_values, recording_device
 
 
 def _chain(seed, n_inputs, n_ops, shape, tweak=None):
@@ -82,3 +82,38 @@ def test_host_values_see_a_changed_constant(tmp_path):
     heavy, vals, ref = _host_and_oracle(tmp_path, 1, 40, 20, (128, 128), tweak=15)
     assert heavy >= 1 and vals is not None
     assert not np.allclose(vals[-1].reshape(ref[-1].shape), ref[-1], rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("transposed,ragged", [(True, False), (True, True), (False, False)])
+def test_gathered_concat_operand_on_host(tmp_path, transposed, ragged):
+    """The dense copy a large DotProd takes of a concat operand: column-major
+    when the pieces run along the product's rows (transposed pieces), else
+    row-major; compared element by element with numpy's concatenation."""
+    from ad_amd.device.hip import codegen
+    ad.reset()
+    rng = np.random.default_rng(3 + ragged)
+    M, N = (257, 130) if ragged else (256, 128)
+    ka = [61, 67, 128] if ragged else [64, 64, 128]
+    if transposed:
+        pieces = [rng.standard_normal((k, M)).astype(np.float32) for k in ka]
+        A = ad.concat([Tensor(x).T() for x in pieces], 1)
+        dense = np.concatenate([x.T for x in pieces], 1)
+    else:
+        pieces = [rng.standard_normal((M, k)).astype(np.float32) for k in ka]
+        A = ad.concat([Tensor(x) for x in pieces], 1)
+        dense = np.concatenate(pieces, 1)
+    B = Tensor(rng.standard_normal((sum(ka), N)).astype(np.float32))
+    Receiver(lambda v: None, [A @ B])
+    assert M * N * sum(ka) >= codegen.GATHER_MIN_MACS
+    dev, arena = host_arena(ad.compile_proc(), str(tmp_path))
+    assert arena is not None, "a launch left the arena"
+    (pid, plans), = [(pid, ps) for pid, ps in dev.kernels.items()
+                     if any(p.family == "dotprod" for p in ps) and ps[0].family == "elw"]
+    gather = plans[0]
+    col_major = "_x = _global_id % " in gather.source
+    assert col_major == transposed
+    dst = next(i for i, a in enumerate(gather.args) if a[0] == "scratch")
+    off = dev._arg_values(gather, pid)[dst][1]
+    got = arena[off:off + 4 * dense.size].view(np.float32)
+    want = dense.T.ravel() if col_major else dense.ravel()
+    assert np.array_equal(got, want)
