@@ -58,79 +58,90 @@ def fill_child_datacmds(node, _):
     return node
 
 
+def _matrix_operand(coords, node, data_cmds, size_hint, in_concat):
+    """A buffer read: ``Global`` when an elementwise read goes straight to
+    the buffer, else the flat index of the source coordinates the chain of
+    data-movement nodes maps ``coords`` to."""
+    if not in_concat and len(data_cmds) == 0 and coords != [X(), Y()]:
+        return KMatrix(node.id, Global(), node.shape)
+    source = ndim_change_datacmds(coords, data_cmds)
+    return KMatrix(node.id, simplify_expr(ndim_to_global(source, node.shape), size_hint), node.shape)
+
+
+def _concat_operand(coords, node, data_cmds, shape):
+    """A concat read as a selection between its two pieces: the second
+    where the coordinate along the concat axis is past the first piece
+    (shifted back by the first piece's extent), else the first."""
+    coords = ndim_change_datacmds(coords, data_cmds)
+    axis = node.dim
+    split = node.children_shapes[0][axis]
+    # fixed before the first piece is built: building a piece may edit the
+    # coordinate list it is given
+    second = deepcopy(coords)
+    second[axis] = Minus(second[axis], Val(Constant(split)))
+    selects_second = deepcopy(MoreThan(coords[axis], Val(Constant(split - 1))))
+    pieces = [make_karg(coords, node.left, node.children_datacmds[0], node.children_shapes[0], is_concat=True)]
+    pieces.append(make_karg(second, node.right, node.children_datacmds[1], node.children_shapes[1],
+                            is_concat=True))
+    return KConcat(pieces[0], pieces[1], condition=selects_second, shape=shape)
+
+
 def make_karg(initial_dim, child, data_cmds, shape, size_hint: Optional[int] = None, is_concat=False):
+    """Kernel operand that reads ``child`` (through the data-movement nodes
+    ``data_cmds``) at the coordinates ``initial_dim`` of the consumer."""
     if isinstance(child, ConstantNode):
         return KConstant(child.constant)
     if isinstance(child, ConcatNode):
-        dim = ndim_change_datacmds(initial_dim, data_cmds)
-        concat_dim = child.dim
-        idx_end = child.children_shapes[0][concat_dim]
-        dim_two = deepcopy(dim)
-        dim_two[concat_dim] = Minus(dim_two[concat_dim], Val(Constant(idx_end)))
-        condition = deepcopy(MoreThan(dim[concat_dim], Val(Constant(idx_end - 1))))
-        karg_one = make_karg(dim, child.left, child.children_datacmds[0], child.children_shapes[0],
-                             is_concat=True)
-        karg_two = make_karg(dim_two, child.right, child.children_datacmds[1], child.children_shapes[1],
-                             is_concat=True)
-        return KConcat(karg_one, karg_two, condition=condition, shape=shape)
-    if not is_concat and len(data_cmds) == 0 and initial_dim != [X(), Y()]:
-        access = Global()
-    else:
-        dim = ndim_change_datacmds(initial_dim, data_cmds)
-        access = simplify_expr(ndim_to_global(dim, child.shape), size_hint)
-    return KMatrix(child.id, access, child.shape)
+        return _concat_operand(initial_dim, child, data_cmds, shape)
+    return _matrix_operand(initial_dim, child, data_cmds, size_hint, is_concat)
 
 
 def make_res_arg(kern_id: int, is_global: bool, shape):
-    if is_global:
-        return KMatrix(kern_id=kern_id, access=Global(), shape=shape)
-    return KMatrix(kern_id=kern_id, access=simplify_expr(ndim_to_global([X(), Y()], shape), None),
-                   shape=shape)
+    """The result of a node: its flat index, or (row, column) of a tile."""
+    access = Global() if is_global else simplify_expr(ndim_to_global([X(), Y()], shape), None)
+    return KMatrix(kern_id=kern_id, access=access, shape=shape)
+
+
+# how a node's operands are read: at the (row, column) of a DotProd or
+# Reduce tile, or at the coordinates of the consumer's flat index
+_TILE, _FLAT = "tile", "flat"
+
+
+def _reads(node):
+    """(operands, index space, size hint per operand, result written by
+    flat index / by tile / not at all) of a node whose operands become
+    kernel args, else None."""
+    if isinstance(node, DotProdNode):
+        return [node.left, node.right], _TILE, [None, None], _TILE
+    if isinstance(node, BinaryNode):
+        n = math.prod(node.shape)
+        return [node.left, node.right], _FLAT, [n, n], _FLAT
+    if isinstance(node, ReduceNode):
+        return [node.child], _TILE, [None], _TILE
+    if isinstance(node, (UnaryNode, ContigiousNode)):
+        return [node.child], _FLAT, [math.prod(node.shape)], _FLAT
+    if isinstance(node, Receiver):
+        return list(node.rec_children), _FLAT, [prod(s) for s in node.children_shapes], None
+    return None
 
 
 def calc_exprs(node, _):
-    if isinstance(node, DotProdNode):
-        if node.children_datacmds is None:
-            return node
-        node.kargs[0] = make_karg([X(), Y()], node.left, node.children_datacmds[0], node.children_shapes[0])
-        node.kargs[1] = make_karg([X(), Y()], node.right, node.children_datacmds[1], node.children_shapes[1])
-        node.kres = make_res_arg(node.id, is_global=False, shape=node.shape)
-        node.children_datacmds = None
-    elif isinstance(node, BinaryNode):
-        if node.children_datacmds is None:
-            return node
-        size = math.prod(node.shape)
-        node.kargs[0] = make_karg(global_to_ndim(Global(), node.children_shapes[0]), node.left,
-                                  node.children_datacmds[0], node.children_shapes[0], size_hint=size)
-        node.kargs[1] = make_karg(global_to_ndim(Global(), node.children_shapes[1]), node.right,
-                                  node.children_datacmds[1], node.children_shapes[1], size_hint=size)
+    """Replace ``node``'s operands and result by kernel args (once: the data
+    command lists are dropped afterwards)."""
+    if isinstance(node, Feeder):
         node.kres = make_res_arg(node.id, is_global=True, shape=node.shape)
-        node.children_datacmds = None
-    elif isinstance(node, ReduceNode):
-        if node.children_datacmds is None:
-            return node
-        node.kargs[0] = make_karg([X(), Y()], node.child, node.children_datacmds[0], node.children_shapes[0])
-        node.kres = make_res_arg(node.id, is_global=False, shape=node.shape)
-        node.children_datacmds = None
-    elif isinstance(node, (UnaryNode, ContigiousNode)):
-        if node.children_datacmds is None:
-            return node
-        size = math.prod(node.shape)
-        node.kargs[0] = make_karg(global_to_ndim(Global(), node.children_shapes[0]), node.child,
-                                  node.children_datacmds[0], node.children_shapes[0], size_hint=size)
-        node.kres = make_res_arg(node.id, is_global=True, shape=node.shape)
-        node.children_datacmds = None
-    elif isinstance(node, Feeder):
-        node.kres = make_res_arg(node.id, is_global=True, shape=node.shape)
-    elif isinstance(node, Receiver):
-        if node.children_datacmds is None:
-            return node
-        ch = node.rec_children
-        for idx in range(len(ch)):
-            node.kargs[idx] = make_karg(global_to_ndim(Global(), node.children_shapes[idx]), ch[idx],
-                                        node.children_datacmds[idx], node.children_shapes[idx],
-                                        size_hint=prod(node.children_shapes[idx]))
-        node.children_datacmds = None
+        return node
+    layout = _reads(node)
+    if layout is None or node.children_datacmds is None:
+        return node
+    operands, space, hints, result = layout
+    for i, (child, hint) in enumerate(zip(operands, hints)):
+        shape = node.children_shapes[i]
+        coords = [X(), Y()] if space == _TILE else global_to_ndim(Global(), shape)
+        node.kargs[i] = make_karg(coords, child, node.children_datacmds[i], shape, size_hint=hint)
+    if result is not None:
+        node.kres = make_res_arg(node.id, is_global=result == _FLAT, shape=node.shape)
+    node.children_datacmds = None
     return node
 
 
