@@ -1,8 +1,12 @@
-"""Structural common-subexpression elimination
-(autodiff/opt/repeat_opt.py:12-72).  Two nodes with the same kind and the
-same operand ids (data-movement chains compared structurally down to the
-source) are merged into the first one found; repeated until nothing merges
-(at most 100 rounds)."""
+"""Structural common-subexpression elimination (the behaviour of
+autodiff/opt/repeat_opt.py:12-72).
+
+Two nodes are interchangeable when their merge keys are equal: the node's
+own ``repeat_helper`` (kind and parameters) after those of its operands
+(a data-movement chain is compared by structure down to its source).  In a
+round, every node is noted under its key in walk order, and every later
+member of a key is replaced by the first; rounds repeat until one merges
+nothing (at most 100)."""
 from typing import Any, Dict, List
 
 from ..graph import ConstantNode, Tensor
@@ -10,46 +14,46 @@ from ..helper import walk_graph
 
 __all__ = ["repeat_opt"]
 
+_MAX_ROUNDS = 100
 
-def _intern_repeat_opt(context) -> int:
-    groups: Dict[Any, List] = {}
 
-    def track_nodes(node, _):
-        if node.get_block() is not None:
-            return node
-        if isinstance(node, Tensor) or isinstance(node, ConstantNode):
-            return node
-        key = tuple([ch.repeat_helper(is_child=True) for ch in node.children()]) \
-            + tuple(node.repeat_helper(is_child=False))
-        if key in groups:
-            groups[key].append(node)
-        else:
-            groups[key] = [node]
+def _mergeable(node) -> bool:
+    """Loops, Tensors and constants are never merged."""
+    return node.get_block() is None and not isinstance(node, (Tensor, ConstantNode))
+
+
+def _merge_key(node):
+    return tuple(operand.repeat_helper(is_child=True) for operand in node.children()) \
+        + tuple(node.repeat_helper(is_child=False))
+
+
+def _one_round(context) -> int:
+    """One round; returns the number of keys noted more than once (a node
+    noted twice under its key counts, as in the reference)."""
+    noted: Dict[Any, List] = {}
+
+    def note(node, _):
+        if _mergeable(node):
+            noted.setdefault(_merge_key(node), []).append(node)
         return node
+    context.procedure[0] = walk_graph(context.procedure[0], note)
 
-    context.procedure[0] = walk_graph(context.procedure[0], track_nodes)
-    dupes = [nodes for nodes in groups.values() if len(nodes) > 1]
-
-    # the first group whose later members include the node's id decides
-    # (the reference scans the groups in order for every node)
-    keep_of = {}
-    for nodes in dupes:
-        for v in nodes[1:]:
-            keep_of.setdefault(v.id, nodes[0])
-
-    def replace_node(node, _):
-        return keep_of.get(node.id, node)
-
-    context.procedure[0] = walk_graph(context.procedure[0], replace_node)
-    return len(dupes)
+    survivor = {}
+    repeated = 0
+    for members in noted.values():
+        if len(members) > 1:
+            repeated += 1
+            for later in members[1:]:
+                survivor.setdefault(later.id, members[0])
+    context.procedure[0] = walk_graph(context.procedure[0], lambda node, _: survivor.get(node.id, node))
+    return repeated
 
 
 def repeat_opt(context):
-    merged = 1
-    rounds = 0
-    while merged > 0:
-        merged = _intern_repeat_opt(context)
-        rounds += 1
-        if rounds >= 100:
+    for rounds in range(1, _MAX_ROUNDS + 1):
+        repeated = _one_round(context)
+        if rounds == _MAX_ROUNDS:
             print("Repeat opt max iteration passed")
-            break
+            return
+        if repeated == 0:
+            return
