@@ -1,27 +1,22 @@
 """Hoist every remaining non-temp, content-free Alloc to the front of the
-main Proc and every non-temp Dealloc to its end
-(autodiff/alloc/clean.py:3-28)."""
+main Proc and every non-temp Dealloc to its end; temp Deallocs are dropped
+(the behaviour of autodiff/alloc/clean.py:3-28)."""
 from . import AllocEntry, DeallocEntry
 
 
 def temp_clean(proc):
     allocs, deallocs = [], []
 
-    def pick(node, _):
-        if isinstance(node, AllocEntry):
-            if node.is_temp or node.content is not None:
-                return node
-            allocs.append(node)
-        elif isinstance(node, DeallocEntry):
+    def sift(node, _):
+        if isinstance(node, DeallocEntry):
             if not node.is_temp:
                 deallocs.append(node)
-            else:
-                return None
-        else:
-            return node
-        return None
-    proc.walk(pick)
-    for a in allocs:
-        proc.insert(0, a)
-    for d in deallocs:
-        proc.append(d)
+            return None                      # a temp's free is implicit (registers)
+        if isinstance(node, AllocEntry) and not node.is_temp and node.content is None:
+            allocs.append(node)
+            return None
+        return node
+    proc.walk(sift)
+    # each collected Alloc goes to the front in turn: the last one first
+    proc.procedure[:0] = allocs[::-1]
+    proc.procedure.extend(deallocs)
