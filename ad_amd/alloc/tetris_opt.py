@@ -120,27 +120,36 @@ def place_reference(entries: List[VarEntry]) -> int:
     return high
 
 
-def tetris_opt(proc):
-    var_tracker: Dict[int, Dict[int, VarEntry]] = {}
-    counter = [0]
+def _lifetimes(proc) -> Dict[int, List[VarEntry]]:
+    """Per Proc id: its packable variables -- non-temp, content-free Allocs
+    that a non-temp Dealloc of the same Proc closes -- as VarEntry spans
+    [Alloc position, Dealloc position) in one count over every command the
+    walk visits, largest first (ties keep their first-Alloc order).  A
+    variable allocated again restarts its span in place."""
+    opened: Dict[int, Dict[int, VarEntry]] = {}
+    position = 0
 
-    def record(node, proc_id):
-        if proc_id not in var_tracker:
-            var_tracker[proc_id] = {}
+    def note(node, proc_id):
+        nonlocal position
+        live = opened.setdefault(proc_id, {})
         if isinstance(node, AllocEntry):
             if not node.is_temp and node.content is None:
-                var_tracker[proc_id][node.id] = VarEntry(node.id, counter[0], None, node.size)
-        elif isinstance(node, DeallocEntry):
-            if node.id in var_tracker[proc_id] and not node.is_temp:
-                var_tracker[proc_id][node.id].end_idx = counter[0]
-        counter[0] += 1
+                live[node.id] = VarEntry(node.id, position, None, node.size)
+        elif isinstance(node, DeallocEntry) and not node.is_temp and node.id in live:
+            live[node.id].end_idx = position
+        position += 1
         return node
-    proc.walk(record)
+    proc.walk(note)
+    spans = {}
+    for proc_id, live in opened.items():
+        closed = [e for e in live.values() if e.end_idx is not None]
+        if closed:
+            spans[proc_id] = sorted(closed, key=lambda e: -e.size)
+    return spans
 
-    for proc_id in var_tracker:
-        var_tracker[proc_id] = {k: v for k, v in var_tracker[proc_id].items() if v.end_idx is not None}
-    by_proc = {proc_id: list(sorted(v.values(), key=lambda x: -x.size))
-               for proc_id, v in var_tracker.items() if len(v) > 0}
+
+def tetris_opt(proc):
+    by_proc = _lifetimes(proc)
 
     max_temp_size = 0
     total_size = 0

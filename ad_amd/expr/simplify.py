@@ -216,10 +216,9 @@ def simpl_expr_inner(expr, size):
 
 
 def simplify_expr(expr, size):
-    """Rewrite to a printed-form fixpoint, then one more pass (simplify.py:158-166)."""
-    start = expr
-    while True:
-        end = simpl_expr_inner(start, size)
-        if str(end) == str(start):
-            return simpl_expr_inner(end, size)
-        start = end
+    """Rewrite until a pass leaves the printed form unchanged, then apply
+    one more pass (the behaviour of simplify.py:158-166)."""
+    prev, cur = expr, simpl_expr_inner(expr, size)
+    while str(cur) != str(prev):
+        prev, cur = cur, simpl_expr_inner(cur, size)
+    return simpl_expr_inner(cur, size)
