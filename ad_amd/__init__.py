@@ -7,6 +7,7 @@ reference's compile passes in the reference's order and hands the finished
 procedural IR to a device backend; the backend is chosen by the ``device``
 argument or the ``AD_DEVICE`` environment variable (``hip`` by default).
 """
+import functools
 import os
 import sys
 from math import prod
@@ -23,12 +24,10 @@ if sys.getrecursionlimit() < 200000:
 
 
 def concat(nodes: List[Tensor], dim: int):
-    """Left-nested ConcatNode chain, skipping empty operands (__init__.py:14-26)."""
-    kept = [n for n in nodes if prod(n.shape) != 0]
-    n = kept[0]
-    for i in range(1, len(kept)):
-        n = ConcatNode(n, kept[i], dim)
-    return n
+    """Left-nested ConcatNode chain along ``dim``, empty operands skipped
+    (the behaviour of __init__.py:14-26)."""
+    return functools.reduce(lambda joined, n: ConcatNode(joined, n, dim),
+                            [n for n in nodes if prod(n.shape) != 0])
 
 
 def dot(left: Node, right: Node) -> Node:
@@ -56,11 +55,12 @@ def compile_proc():
     proc = mem_opt(proc)
     alloc(proc)
 
-    def assign_program_id(n, _):
-        if isinstance(n, Node) or isinstance(n, FuseBase):
-            n.program_id = context.get_prog_id()
-        return n
-    proc.walk(assign_program_id, step_fused=False, step_proc=True)
+    def number(cmd, _):
+        # every command, loop bodies included, fused groups as one
+        if isinstance(cmd, (Node, FuseBase)):
+            cmd.program_id = context.get_prog_id()
+        return cmd
+    proc.walk(number, step_fused=False, step_proc=True)
     return proc
 
 
