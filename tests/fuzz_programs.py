@@ -32,10 +32,17 @@ def _np_reduce(a, axis, op):
     return out
 
 
+ALL_KINDS = ("unary", "binary", "scalar", "transpose", "slice", "concat", "reduce", "dot", "broadcast")
+# operations whose kernels exchange no data between lanes (no reduction tree,
+# no matrix product): their programs compute real values on the host too
+LANE_INDEPENDENT_KINDS = ("unary", "binary", "scalar", "transpose", "slice", "concat", "broadcast")
+
+
 class _Prog:
-    def __init__(self, rng, grads):
+    def __init__(self, rng, grads, kinds=ALL_KINDS):
         self.rng = rng
         self.grads = grads
+        self.kinds = list(kinds)
         self.vals = []          # (node, float64 array)
         self.inputs = []
 
@@ -60,8 +67,7 @@ class _Prog:
 
     def step(self):
         rng = self.rng
-        kind = rng.choice(["unary", "binary", "scalar", "transpose", "slice", "concat", "reduce", "dot",
-                           "broadcast"])
+        kind = rng.choice(self.kinds)
         if kind == "unary":
             x, a = self.pick()
             u = rng.choice(["sin", "exp2", "recip", "log2", "sqrt", "relu", "sigmoid", "gt"])
@@ -136,13 +142,14 @@ class _Prog:
         return None
 
 
-def random_program(seed, n_ops=8, grads=False):
-    """Trace one random program; returns ``(got, expected)``: ``got`` is
-    filled by Receivers when the program executes, ``expected`` holds the
-    float64 values of the received outputs (None for input gradients, which
-    only a second backend can check)."""
+def random_program(seed, n_ops=8, grads=False, kinds=ALL_KINDS):
+    """Trace one random program drawing its operations from ``kinds``;
+    returns ``(got, expected)``: ``got`` is filled by Receivers when the
+    program executes, ``expected`` holds the float64 values of the received
+    outputs (None for input gradients, which only a second backend can
+    check)."""
     rng = np.random.default_rng(seed)
-    p = _Prog(rng, grads)
+    p = _Prog(rng, grads, kinds)
     made = []
     while len(made) < n_ops:
         v = p.step()

@@ -117,3 +117,22 @@ def test_gathered_concat_operand_on_host(tmp_path, transposed, ragged):
     got = arena[off:off + 4 * dense.size].view(np.float32)
     want = dense.T.ravel() if col_major else dense.ravel()
     assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_lane_independent_programs_on_host(tmp_path, seed):
+    """Random chains of unary, binary, scalar, transpose, slice, concat and
+    broadcast operations (the fuzz generator restricted to lane-independent
+    kinds; float4 and scalar passes, concat conditions, permuted and sliced
+    reads): every received value of the host run equals the oracle's."""
+    from .fuzz_programs import LANE_INDEPENDENT_KINDS, random_program
+    ad.reset()
+    random_program(3000 + seed, n_ops=14, kinds=LANE_INDEPENDENT_KINDS)
+    vals = host_values(ad.compile_proc(), str(tmp_path))
+    assert vals is not None, "a launch left the arena"
+    ad.reset()
+    ref, _ = random_program(3000 + seed, n_ops=14, kinds=LANE_INDEPENDENT_KINDS)
+    ad.execute(device=OracleDevice())
+    assert len(vals) >= len(ref["outs"])
+    for got, want in zip(vals, ref["outs"]):
+        np.testing.assert_allclose(got.reshape(want.shape), want, rtol=1e-5, atol=1e-6)
