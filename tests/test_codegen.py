@@ -618,3 +618,24 @@ def test_balanced_concat_selects_the_same_piece(pieces):
     bal2 = codegen.balance_concat(rows)
     for g in list(range(0, 3000, 13)):
         assert select(bal2, g)[0] == select(rows, g)[0]
+
+
+def test_narrow_launch_policy():
+    """dp_quad alternatives: 64 x 64-tile products with K chunks of at least
+    QUAD_MIN_CHUNK terms (64-deep panels below 128 terms), taken by launch
+    groups of at most NARROW_MAX_BLOCKS 64 x 64 blocks."""
+    from ad_amd.device.hip.codegen import NARROW_MAX_BLOCKS, dp_config, quad_config, use_narrow
+    # the C5 per-(sample, head) products and the split per-head weight gradient
+    assert quad_config(512, 64, 512, dp_config(512, 64, 512)) == (32, 32, 1, 128)
+    assert quad_config(512, 512, 64, dp_config(512, 512, 64)) == (32, 32, 1, 64)
+    cfg = dp_config(1024, 64, 4096)
+    assert cfg[:3] == (64, 64, 8) and quad_config(1024, 64, 4096, cfg) == (32, 32, 8, 128)
+    # 128 x 128 tiles, skinny and direct products get none
+    assert quad_config(4096, 4096, 4096, dp_config(4096, 4096, 4096)) is None
+    assert quad_config(8, 255, 255, (64, 64, 1, 64)) is None
+    assert quad_config(255, 255, 2, (64, 64, 1, 64)) is None
+    from types import SimpleNamespace
+    plan = SimpleNamespace(grid=(1, 8, 1), narrow=None)       # 8 blocks of 64 x 64 per product
+    assert not use_narrow(plan, 1)                            # no alternative
+    plan.narrow = SimpleNamespace(grid=(2, 16, 1), narrow=None)
+    assert use_narrow(plan, NARROW_MAX_BLOCKS // 8) and not use_narrow(plan, NARROW_MAX_BLOCKS // 8 + 1)
