@@ -5,13 +5,16 @@ then runs on the host over one arena of the device's size, compiled with
 AddressSanitizer, so any global or LDS access outside its allocation is
 reported with the kernel that made it.
 
-Only addresses are checked: every kernel's addresses are functions of its
-indices alone, so cross-lane exchanges and matrix products return their own
-input, barriers do nothing, and the threads of a block run one after
-another.  Loop bodies replay as recorded graphs (with their Feeder staging
-and Receiver snapshot copies), and the argument-table rows each launch
-reads are checked against the table the device wrote.  Test
-infrastructure; nothing in the package imports it."""
+By default only addresses are checked: every kernel's addresses are
+functions of its indices alone, so cross-lane exchanges and matrix products
+return their own input, barriers do nothing, and the threads of a block run
+one after another (elementwise passes still compute their real values,
+``host_values``).  With ``lockstep`` the threads of a block run together with
+real barriers, shuffles and fp32 MFMAs (``LOCKSTEP_SHIM``), so DotProd
+kernels compute their real values too.  Loop bodies replay as recorded
+graphs (with their Feeder staging and Receiver snapshot copies), and the
+argument-table rows each launch reads are checked against the table the
+device wrote.  Test infrastructure; nothing in the package imports it."""
 import hashlib
 import os
 import re
@@ -58,6 +61,104 @@ template <class F> static void adhip_launch(F f, const unsigned long long* t, un
   for (unsigned z = 0; z < gz; ++z) for (unsigned y = 0; y < gy; ++y) for (unsigned x = 0; x < gx; ++x) {
     blockIdx = {x, y, z};
     for (unsigned t2 = 0; t2 < bx; ++t2) { threadIdx = {t2, 0, 0}; f(t); }
+  }
+}
+"""
+
+
+# The same kernels with real values: every thread of a block runs on its own
+# OS thread; __syncthreads is a block barrier; a wavefront-scope fence is a
+# wave barrier; a shuffle or an fp32 MFMA exchanges the wave's values between
+# two wave barriers.  v_mfma_f32_32x32x2f32
+# takes A[i][k] from lane i + 32k and B[k][j] from lane j + 32k and returns,
+# in lane l's element r, row 8*(r/4) + 4*(l/32) + r%4 of column l%32 of
+# C + A*B.  A barrier waited on for 20 s aborts (a divergent barrier would
+# otherwise hang).  Blocks run one after another.
+LOCKSTEP_SHIM = r"""
+#include <cstdint>
+#include <cstddef>
+#include <cstdio>
+#include <cstdlib>
+#include <cmath>
+#include <cstring>
+#include <thread>
+#include <mutex>
+#include <condition_variable>
+#include <chrono>
+#include <vector>
+#define __global__
+#define __device__
+#define __host__
+#define __forceinline__ inline
+#define __launch_bounds__(...)
+#define __shared__ static
+struct adhip_dim3 { unsigned x, y, z; };
+static thread_local adhip_dim3 threadIdx, blockIdx;
+static adhip_dim3 blockDim, gridDim;
+struct float4 { float x, y, z, w; };
+static inline float4 make_float4(float a, float b, float c, float d) { float4 r; r.x = a; r.y = b; r.z = c; r.w = d; return r; }
+struct uint4 { unsigned x, y, z, w; };
+typedef float adhip_v16 __attribute__((ext_vector_type(16)));
+struct adhip_barrier {
+  std::mutex m; std::condition_variable cv; unsigned n = 0, count = 0, gen = 0;
+  void wait() {
+    std::unique_lock<std::mutex> lk(m);
+    unsigned g = gen;
+    if (++count == n) { count = 0; ++gen; cv.notify_all(); return; }
+    if (!cv.wait_for(lk, std::chrono::seconds(20), [&] { return gen != g; })) {
+      fprintf(stderr, "barrier timeout\n"); abort();
+    }
+  }
+};
+static adhip_barrier adhip_block_bar;
+static adhip_barrier adhip_wave_bar[16];
+static float adhip_wave_a[16][64], adhip_wave_b[16][64];
+static inline unsigned adhip_lane() { return threadIdx.x & 63u; }
+static inline unsigned adhip_wave() { return threadIdx.x >> 6; }
+#define __syncthreads() adhip_block_bar.wait()
+template <class T> static inline T __shfl_xor(T v, int off, int width = 64) {
+  const unsigned l = adhip_lane(), w = adhip_wave();
+  float* buf = adhip_wave_a[w];
+  T out;
+  memcpy(&buf[l], &v, sizeof(float));
+  adhip_wave_bar[w].wait();
+  const unsigned src = (l & ~(unsigned)(width - 1)) | ((l ^ (unsigned)off) & (unsigned)(width - 1));
+  memcpy(&out, &buf[src], sizeof(float));
+  adhip_wave_bar[w].wait();
+  return out;
+}
+static inline adhip_v16 adhip_mfma_32x32x2(float a, float b, adhip_v16 c) {
+  const unsigned l = adhip_lane(), w = adhip_wave();
+  adhip_wave_a[w][l] = a; adhip_wave_b[w][l] = b;
+  adhip_wave_bar[w].wait();
+  adhip_v16 d = c;
+  const unsigned col = l & 31u;
+  for (int r = 0; r < 16; ++r) {
+    const unsigned row = 8u * (r >> 2) + 4u * (l >> 5) + (r & 3);
+    d[r] = c[r] + (adhip_wave_a[w][row] * adhip_wave_b[w][col] + adhip_wave_a[w][row + 32] * adhip_wave_b[w][col + 32]);
+  }
+  adhip_wave_bar[w].wait();
+  return d;
+}
+// a wave executes in lockstep on the GPU: the kernels order LDS traffic
+// between the lanes of a wave with wavefront-scope fences alone
+#define __builtin_amdgcn_fence(...) adhip_wave_bar[adhip_wave()].wait()
+#define __builtin_amdgcn_iglp_opt(...) ((void)0)
+#define __builtin_amdgcn_s_setprio(...) ((void)0)
+#define __builtin_amdgcn_sched_barrier(...) ((void)0)
+#define __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, ...) adhip_mfma_32x32x2((a), (b), (c))
+#define __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, ...) (c)
+using std::exp2; using std::log2; using std::sin; using std::sqrt; using std::fabs;
+template <class F> static void adhip_launch(F f, const unsigned long long* t, unsigned gx, unsigned gy,
+                                            unsigned gz, unsigned bx) {
+  gridDim = {gx, gy, gz}; blockDim = {bx, 1, 1};
+  adhip_block_bar.n = bx;
+  for (unsigned w = 0; w < 16; ++w) adhip_wave_bar[w].n = (bx - 64 * w) < 64 ? (bx > 64 * w ? bx - 64 * w : 0) : 64;
+  for (unsigned z = 0; z < gz; ++z) for (unsigned y = 0; y < gy; ++y) for (unsigned x = 0; x < gx; ++x) {
+    std::vector<std::thread> lanes;
+    for (unsigned t2 = 0; t2 < bx; ++t2)
+      lanes.emplace_back([=] { blockIdx = {x, y, z}; threadIdx = {t2, 0, 0}; f(t); });
+    for (auto& th : lanes) th.join();
   }
 }
 """
@@ -268,7 +369,7 @@ def _host_source(src):
     return re.sub(r"__attribute__\(\(address_space\(\d\)\)\)", "", src)
 
 
-def check_run(proc, workdir, shrink=None, device=None, dump=None, **device_options):
+def check_run(proc, workdir, shrink=None, device=None, dump=None, lockstep=False, **device_options):
     """Run ``proc`` through a recording HIPDevice (loops replayed as
     recorded graphs), then check transfers and argument tables
     (``check_tables``) and run every launch on the host under
@@ -299,7 +400,7 @@ def check_run(proc, workdir, shrink=None, device=None, dump=None, **device_optio
         blob[off:off + len(data)] = data
     size = ctx.size - (shrink or 0)
     used = {op[1] for op in launches if op[0] == "launch"}
-    text = [SHIM, _host_source(open(HEADER_PATH).read())]
+    text = [LOCKSTEP_SHIM if lockstep else SHIM, _host_source(open(HEADER_PATH).read())]
     for i, (name, src) in enumerate(sources.items()):
         if name in used:
             text.append(f"namespace k{i} {{\n{_host_source(src)}\n}}\nusing k{i}::{name};")
@@ -336,7 +437,8 @@ def check_run(proc, workdir, shrink=None, device=None, dump=None, **device_optio
     with open(exe + ".cpp", "w") as fh:
         fh.write(code)
     r = subprocess.run([CLANG, "-std=c++17", "-O1", "-g", "-fsanitize=address", "-fno-omit-frame-pointer",
-                        "-Wno-everything", exe + ".cpp", "-o", exe], capture_output=True, text=True)
+                        "-Wno-everything", *(["-pthread"] if lockstep else []), exe + ".cpp", "-o", exe],
+                       capture_output=True, text=True)
     if r.returncode != 0:
         return False, "host build failed:\n" + r.stderr[-3000:]
     env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0")
@@ -344,17 +446,19 @@ def check_run(proc, workdir, shrink=None, device=None, dump=None, **device_optio
     return r.returncode == 0 and "all launches in bounds" in r.stderr, r.stderr[-4000:]
 
 
-def host_arena(proc, workdir, **device_options):
+def host_arena(proc, workdir, lockstep=False, **device_options):
     """Run ``proc``'s launches on the host (``check_run``) and return the
     recording device and the arena bytes after the last launch (None if a
     launch leaves the arena)."""
     dump = os.path.join(workdir, "arena_after.bin")
     dev = recording_device(**device_options)
-    ok, log = check_run(proc, workdir, device=dev, dump=dump)
+    ok, log = check_run(proc, workdir, device=dev, dump=dump, lockstep=lockstep)
+    if not ok:
+        print(log[-2000:])
     return dev, (np.fromfile(dump, dtype=np.uint8) if ok else None)
 
 
-def host_values(proc, workdir, **device_options):
+def host_values(proc, workdir, lockstep=False, **device_options):
     """Values of every host read (Receiver) of a Proc computed by running its
     launches on the host, in read order; None if a launch leaves the arena.
     Only kernels whose lanes do not exchange data (elementwise passes,
@@ -362,7 +466,7 @@ def host_values(proc, workdir, **device_options):
     builtins return their inputs and a block's threads run one after
     another.  Each distinct launch runs once, so a Proc with loops gives
     the values of one pass through each body."""
-    dev, arena = host_arena(proc, workdir, **device_options)
+    dev, arena = host_arena(proc, workdir, lockstep=lockstep, **device_options)
     if arena is None:
         return None
     return [arena[off:off + nb].view(np.float32).copy() for off, nb in dev.ctx.reads]
