@@ -56,15 +56,15 @@ def test_tile_kernels_on_host(tmp_path, M, K, N, ta, tb, epilogue, kernel):
     assert kernel in src
 
 
-@pytest.mark.parametrize("M,K,N,ta,tb,epilogue", [
-    (256, 512, 64, False, False, True),      # one 128-deep panel per wave and round, 4 rounds
-    (130, 300, 257, True, True, True),       # ragged K: a partial last panel
-    (64, 1024, 64, False, True, False),      # K split in 4 chunks of 256, then the combine pass
-    (512, 64, 100, True, False, True),       # K = 64: 64-deep panels
+@pytest.mark.parametrize("M,K,N,ta,tb,epilogue,kernel", [
+    (256, 512, 64, False, False, True, "dp_quad<1, 128>"),   # one 128-deep panel per wave and round, 4 rounds
+    (130, 300, 257, True, True, True, "dp_quad<1, 128>"),    # ragged K: a partial last panel
+    (64, 1024, 64, False, True, False, "dp_quad<4, 128>"),   # K split in 4 chunks of 256, then the combine pass
+    (512, 64, 100, True, False, True, "dp_quad<1, 64>"),     # K = 64: 64-deep panels
 ])
-def test_quad_kernel_on_host(tmp_path, M, K, N, ta, tb, epilogue):
+def test_quad_kernel_on_host(tmp_path, M, K, N, ta, tb, epilogue, kernel):
     """dp_quad, the kernel of launch groups too small to fill the device
     (32 x 32 tiles, each block's K panels split among its four waves, the
     partial tiles added through LDS)."""
     src = _run(tmp_path, M, K, N, ta, tb, epilogue)
-    assert "dp_quad<" in src
+    assert kernel in src
