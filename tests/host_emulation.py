@@ -14,7 +14,11 @@ real barriers, shuffles and fp32 MFMAs (``LOCKSTEP_SHIM``), so DotProd
 kernels compute their real values too.  Loop bodies replay as recorded
 graphs (with their Feeder staging and Receiver snapshot copies), and the
 argument-table rows each launch reads are checked against the table the
-device wrote.  Test infrastructure; nothing in the package imports it."""
+device wrote.  A bounds check runs each distinct launch once; a value run
+(``host_values``) replays the device's whole sequence in call order --
+every iteration, the Feeder data staged for it, every host read and
+Receiver fetch -- so whole training loops can be compared with the oracle.
+Test infrastructure; nothing in the package imports it."""
 import hashlib
 import os
 import re
@@ -200,10 +204,12 @@ class RecordingContext:
         if self._capture is not None:
             self.errors.append(("host write during capture", off, arr.nbytes, self.size))
         self.writes.append((off, arr.tobytes()))
+        self.launches.append(("write", off, arr.tobytes()))
 
     def read(self, off, out):
         self._check(off, out.nbytes, "read")
         self.reads.append((off, out.nbytes))
+        self.launches.append(("read", off, out.nbytes))
 
     def copy(self, dst, src, n):
         self._check(dst, n, "copy to")
@@ -255,7 +261,9 @@ class RecordingContext:
     def stage_write(self, tag, off, arr):
         if not self._staging.get(tag):
             self.errors.append(("staged write to a closed set", tag, off, self.size))
-        self._check(off, np.asarray(arr).nbytes, "staged write")
+        arr = np.ascontiguousarray(arr, dtype=np.float32)
+        self._check(off, arr.nbytes, "staged write")
+        self.launches.append(("write", off, arr.tobytes()))
 
     def stage_end(self, tag):
         self._staging[tag] = False
@@ -276,6 +284,7 @@ class RecordingContext:
     def fetch_copy(self, fset, off, nbytes):
         f = self._fetch[fset]
         self._check(off, nbytes, "fetch from")
+        self._sink().append(("read", off, nbytes))
         host = f[1]
         f[1] += (nbytes + 255) // 256 * 256
         if f[1] > f[0]:
@@ -369,14 +378,22 @@ def _host_source(src):
     return re.sub(r"__attribute__\(\(address_space\(\d\)\)\)", "", src)
 
 
-def check_run(proc, workdir, shrink=None, device=None, dump=None, lockstep=False, **device_options):
+def check_run(proc, workdir, shrink=None, device=None, dump=None, lockstep=False, full=False,
+              **device_options):
     """Run ``proc`` through a recording HIPDevice (loops replayed as
     recorded graphs), then check transfers and argument tables
     (``check_tables``) and run every launch on the host under
     AddressSanitizer.  ``device`` reuses a recording device (a second
     program on one device); ``shrink`` (bytes) cuts the host arena short, to
     show the check catches an access past it; ``dump`` (a path) receives the
-    arena after the last launch.  Returns ``(ok, log)``."""
+    arena after the last launch.
+
+    By default each distinct launch runs once (a graph replay repeats the
+    same addresses) over an arena holding every host write from the start.
+    With ``full`` the run is the device's own, in call order: every replay's
+    launches and copies, host writes and staged Feeder data applied when
+    they were made, and every host read and Receiver fetch saved when it was
+    made (to ``reads.bin`` in ``workdir``, in order).  Returns ``(ok, log)``."""
     dev = device or recording_device(**device_options)
     mark = len(dev.ctx.launches)
     dev.ctx.writes = []
@@ -415,20 +432,42 @@ def check_run(proc, workdir, shrink=None, device=None, dump=None, lockstep=False
     text.append(f"  unsigned long long* tab = (unsigned long long*)(a + {dev.table_off}ull);")
     text.append(f"  for (size_t i = 0; i < {table_words}ull; ++i)"
                 f" if (tab[i] >= {FAKE_BASE}ull) tab[i] = (unsigned long long)(a + (tab[i] - {FAKE_BASE}ull));")
-    # one call per distinct launch: replays of a graph repeat the same
-    # addresses, so each (kernel, grid, row) is checked once
+    if full:
+        # host data of the writes made after set-up, applied in call order
+        # (the argument table keeps its rewritten pointers)
+        data = b"".join(op[2] for op in launches if op[0] == "write" and op[1] != dev.table_off)
+        data_path = os.path.join(workdir, f"writes_{hashlib.sha1(data).hexdigest()[:12]}.bin")
+        with open(data_path, "wb") as fh:
+            fh.write(data)
+        text.append(f"  unsigned char* wd = (unsigned char*)malloc({len(data)}ull + 1);")
+        text.append(f'  fh = fopen("{data_path}", "rb"); if (!fh || fread(wd, 1, {len(data)}ull, fh) != {len(data)}ull) return 5; fclose(fh);')
+        text.append(f'  FILE* rd = fopen("{os.path.join(workdir, "reads.bin")}", "wb"); if (!rd) return 6;')
+    # without ``full``, one call per distinct launch: replays of a graph
+    # repeat the same addresses, so each (kernel, grid, row) is checked once
     seen = set()
+    pos = 0
     for k, op in enumerate(launches):
         if op[0] == "copy":
             _, dst, src, nb = op
             text.append(f"  memmove(a + {dst}ull, a + {src}ull, {nb}ull);")
             continue
+        if op[0] == "write":
+            if full and op[1] != dev.table_off:
+                text.append(f"  memcpy(a + {op[1]}ull, wd + {pos}ull, {len(op[2])}ull);")
+                pos += len(op[2])
+            continue
+        if op[0] == "read":
+            if full:
+                text.append(f"  if (fwrite(a + {op[1]}ull, 1, {op[2]}ull, rd) != {op[2]}ull) return 7;")
+            continue
         _, func, grid, block, shared, row = op
-        if (func, grid, row) in seen:
+        if not full and (func, grid, row) in seen:
             continue
         seen.add((func, grid, row))
         text.append(f'  fprintf(stderr, "launch {k} {func}\\n"); adhip_launch({func}, '
                     f"(const unsigned long long*)(a + {row - FAKE_BASE}ull), {grid[0]}, {grid[1]}, {grid[2]}, {block[0]});")
+    if full:
+        text.append("  fclose(rd);")
     if dump:
         text.append(f'  {{ FILE* out = fopen("{dump}", "wb"); if (!out || fwrite(a, 1, n, out) != n) return 4; fclose(out); }}')
     text.append('  fprintf(stderr, "all launches in bounds\\n");\n  return 0;\n}')
@@ -446,27 +485,35 @@ def check_run(proc, workdir, shrink=None, device=None, dump=None, lockstep=False
     return r.returncode == 0 and "all launches in bounds" in r.stderr, r.stderr[-4000:]
 
 
-def host_arena(proc, workdir, lockstep=False, **device_options):
+def host_arena(proc, workdir, lockstep=False, full=False, **device_options):
     """Run ``proc``'s launches on the host (``check_run``) and return the
     recording device and the arena bytes after the last launch (None if a
     launch leaves the arena)."""
     dump = os.path.join(workdir, "arena_after.bin")
     dev = recording_device(**device_options)
-    ok, log = check_run(proc, workdir, device=dev, dump=dump, lockstep=lockstep)
+    ok, log = check_run(proc, workdir, device=dev, dump=dump, lockstep=lockstep, full=full)
     if not ok:
         print(log[-2000:])
     return dev, (np.fromfile(dump, dtype=np.uint8) if ok else None)
 
 
 def host_values(proc, workdir, lockstep=False, **device_options):
-    """Values of every host read (Receiver) of a Proc computed by running its
-    launches on the host, in read order; None if a launch leaves the arena.
-    Only kernels whose lanes do not exchange data (elementwise passes,
-    operand gathers, copies) compute real values here: cross-lane and MFMA
-    builtins return their inputs and a block's threads run one after
-    another.  Each distinct launch runs once, so a Proc with loops gives
-    the values of one pass through each body."""
-    dev, arena = host_arena(proc, workdir, lockstep=lockstep, **device_options)
+    """Values of every host read of a Proc (top-level Receivers, Receivers
+    inside loops once per iteration, the final Tensor read-back) computed
+    by running the device's whole run on the host (``check_run`` with
+    ``full``), in the order the device made them; None if a launch leaves
+    the arena.  Without ``lockstep`` only kernels whose lanes do not
+    exchange data (elementwise passes, operand gathers, copies) compute
+    real values: cross-lane and MFMA builtins return their inputs and a
+    block's threads run one after another."""
+    dev, arena = host_arena(proc, workdir, lockstep=lockstep, full=True, **device_options)
     if arena is None:
         return None
-    return [arena[off:off + nb].view(np.float32).copy() for off, nb in dev.ctx.reads]
+    blob = np.fromfile(os.path.join(workdir, "reads.bin"), dtype=np.uint8)
+    out, at = [], 0
+    for op in dev.ctx.launches:
+        if op[0] == "read":
+            out.append(blob[at:at + op[2]].view(np.float32).copy())
+            at += op[2]
+    assert at == blob.size
+    return out
