@@ -6,7 +6,8 @@ their real results.  This checks the generated statement code itself on the
 CPU -- including heavy passes (more statements than
 ``codegen.SCALAR_MIN_STMTS`` over at most ``SCALAR_MAX_N`` elements), whose
 operand reads are issued in batches ahead of the statements -- before any
-GPU run."""
+GPU run.  Random programs of every kind (DotProds and reductions included)
+run with lockstep blocks, which compute cross-lane and MFMA results too."""
 import numpy as np
 import pytest
 
@@ -136,3 +137,24 @@ def test_random_lane_independent_programs_on_host(tmp_path, seed):
     assert len(vals) >= len(ref["outs"])
     for got, want in zip(vals, ref["outs"]):
         np.testing.assert_allclose(got.reshape(want.shape), want, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("seed", [0, 3, 7, 12, 17, 25, 1001, 1006, 1011, 1016])
+def test_random_programs_in_lockstep_on_host(tmp_path, seed):
+    """Random programs of every kind the generator has (DotProds and
+    reductions included; gradients from seed 1000 on, as in the GPU fuzz
+    test), run on the host with lockstep blocks: every received value
+    equals the oracle's to the GPU test's tolerance."""
+    from .fuzz_programs import random_program
+    grads = seed >= 1000
+    ad.reset()
+    random_program(seed, grads=grads)
+    vals = host_values(ad.compile_proc(), str(tmp_path), lockstep=True)
+    assert vals is not None, "a launch left the arena or a barrier timed out"
+    ad.reset()
+    ref, _ = random_program(seed, grads=grads)
+    ad.execute(device=OracleDevice())
+    assert len(vals) >= len(ref["outs"])
+    for got, want in zip(vals, ref["outs"]):
+        scale = max(1.0, float(np.abs(want).max()) if want.size else 1.0)
+        np.testing.assert_allclose(got.reshape(want.shape), want, rtol=1e-4, atol=1e-4 * scale)
