@@ -90,6 +90,7 @@ LOCKSTEP_SHIM = r"""
 #include <condition_variable>
 #include <chrono>
 #include <vector>
+#include <functional>
 #define __global__
 #define __device__
 #define __host__
@@ -153,17 +154,48 @@ static inline adhip_v16 adhip_mfma_32x32x2(float a, float b, adhip_v16 c) {
 #define __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, ...) adhip_mfma_32x32x2((a), (b), (c))
 #define __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, ...) (c)
 using std::exp2; using std::log2; using std::sin; using std::sqrt; using std::fabs;
+// one OS thread per thread of a block, kept across blocks and launches:
+// run(n, job) hands job(i) to threads 0..n-1 and returns when all are done
+struct adhip_pool {
+  std::mutex m; std::condition_variable go, fin;
+  std::vector<std::thread> lanes;
+  unsigned gen = 0, active = 0, left = 0;
+  std::function<void(unsigned)> job;
+  void work(unsigned i) {
+    unsigned seen = 0;
+    for (;;) {
+      std::function<void(unsigned)> j;
+      {
+        std::unique_lock<std::mutex> lk(m);
+        go.wait(lk, [&] { return gen != seen; });
+        seen = gen;
+        if (i >= active) continue;
+        j = job;
+      }
+      j(i);
+      std::lock_guard<std::mutex> lk(m);
+      if (--left == 0) fin.notify_one();
+    }
+  }
+  void run(unsigned n, std::function<void(unsigned)> f) {
+    while (lanes.size() < n) {
+      const unsigned i = lanes.size();
+      lanes.emplace_back([this, i] { work(i); });
+    }
+    std::unique_lock<std::mutex> lk(m);
+    job = std::move(f); active = n; left = n; ++gen;
+    go.notify_all();
+    fin.wait(lk, [&] { return left == 0; });
+  }
+};
+static adhip_pool* adhip_lanes = new adhip_pool;   // never destroyed: its threads wait at exit
 template <class F> static void adhip_launch(F f, const unsigned long long* t, unsigned gx, unsigned gy,
                                             unsigned gz, unsigned bx) {
   gridDim = {gx, gy, gz}; blockDim = {bx, 1, 1};
   adhip_block_bar.n = bx;
   for (unsigned w = 0; w < 16; ++w) adhip_wave_bar[w].n = (bx - 64 * w) < 64 ? (bx > 64 * w ? bx - 64 * w : 0) : 64;
-  for (unsigned z = 0; z < gz; ++z) for (unsigned y = 0; y < gy; ++y) for (unsigned x = 0; x < gx; ++x) {
-    std::vector<std::thread> lanes;
-    for (unsigned t2 = 0; t2 < bx; ++t2)
-      lanes.emplace_back([=] { blockIdx = {x, y, z}; threadIdx = {t2, 0, 0}; f(t); });
-    for (auto& th : lanes) th.join();
-  }
+  for (unsigned z = 0; z < gz; ++z) for (unsigned y = 0; y < gy; ++y) for (unsigned x = 0; x < gx; ++x)
+    adhip_lanes->run(bx, [=](unsigned i) { blockIdx = {x, y, z}; threadIdx = {i, 0, 0}; f(t); });
 }
 """
 
