@@ -10,7 +10,7 @@ functions of its indices alone, so cross-lane exchanges and matrix products
 return their own input, barriers do nothing, and the threads of a block run
 one after another (elementwise passes still compute their real values,
 ``host_values``).  With ``lockstep`` the threads of a block run together with
-real barriers, shuffles and fp32 MFMAs (``LOCKSTEP_SHIM``), so DotProd
+real barriers, shuffles and fp32 and bf16 MFMAs (``LOCKSTEP_SHIM``), so DotProd
 kernels compute their real values too.  Loop bodies replay as recorded
 graphs (with their Feeder staging and Receiver snapshot copies), and the
 argument-table rows each launch reads are checked against the table the
@@ -76,7 +76,8 @@ template <class F> static void adhip_launch(F f, const unsigned long long* t, un
 # two wave barriers.  v_mfma_f32_32x32x2f32
 # takes A[i][k] from lane i + 32k and B[k][j] from lane j + 32k and returns,
 # in lane l's element r, row 8*(r/4) + 4*(l/32) + r%4 of column l%32 of
-# C + A*B.  A barrier waited on for 20 s aborts (a divergent barrier would
+# C + A*B; v_mfma_f32_32x32x16_bf16 takes eight k per lane (k = 8*(l/32) + v)
+# and returns the same layout.  A barrier waited on for 20 s aborts (a divergent barrier would
 # otherwise hang).  Blocks run one after another.
 LOCKSTEP_SHIM = r"""
 #include <cstdint>
@@ -145,6 +146,26 @@ static inline adhip_v16 adhip_mfma_32x32x2(float a, float b, adhip_v16 c) {
   adhip_wave_bar[w].wait();
   return d;
 }
+// v_mfma_f32_32x32x16_bf16: lane l holds A[l%32][8*(l/32) + v] and
+// B[k][l%32] with k = 8*(l/32) + v in element v of its operands; the
+// results layout is the fp32 MFMA's
+static float adhip_wave_a8[16][64][8], adhip_wave_b8[16][64][8];
+template <class V> static inline adhip_v16 adhip_mfma_32x32x16_bf16(V a, V b, adhip_v16 c) {
+  const unsigned l = adhip_lane(), w = adhip_wave();
+  for (int v = 0; v < 8; ++v) { adhip_wave_a8[w][l][v] = (float)a[v]; adhip_wave_b8[w][l][v] = (float)b[v]; }
+  adhip_wave_bar[w].wait();
+  adhip_v16 d = c;
+  const unsigned col = l & 31u;
+  for (int r = 0; r < 16; ++r) {
+    const unsigned row = 8u * (r >> 2) + 4u * (l >> 5) + (r & 3);
+    float sum = 0.f;
+    for (int h = 0; h < 2; ++h)
+      for (int v = 0; v < 8; ++v) sum += adhip_wave_a8[w][row + 32 * h][v] * adhip_wave_b8[w][col + 32 * h][v];
+    d[r] = c[r] + sum;
+  }
+  adhip_wave_bar[w].wait();
+  return d;
+}
 // a wave executes in lockstep on the GPU: the kernels order LDS traffic
 // between the lanes of a wave with wavefront-scope fences alone
 #define __builtin_amdgcn_fence(...) adhip_wave_bar[adhip_wave()].wait()
@@ -152,7 +173,7 @@ static inline adhip_v16 adhip_mfma_32x32x2(float a, float b, adhip_v16 c) {
 #define __builtin_amdgcn_s_setprio(...) ((void)0)
 #define __builtin_amdgcn_sched_barrier(...) ((void)0)
 #define __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, ...) adhip_mfma_32x32x2((a), (b), (c))
-#define __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, ...) (c)
+#define __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, ...) adhip_mfma_32x32x16_bf16((a), (b), (c))
 using std::exp2; using std::log2; using std::sin; using std::sqrt; using std::fabs;
 // one OS thread per thread of a block, kept across blocks and launches:
 // run(n, job) hands job(i) to threads 0..n-1 and returns when all are done

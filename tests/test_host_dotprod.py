@@ -3,8 +3,9 @@ on its own OS thread, real barriers, the fp32 MFMA and cross-lane shuffles
 emulated with the hardware's lane layout; ``host_emulation.LOCKSTEP_SHIM``)
 against float64 numpy: the MFMA tile kernels (64 x 64 and 128 x 128 tiles,
 split K with its combine pass), ``dp_quad`` for small launch groups, the
-skinny and direct kernels, transposed operands and fused epilogues -- the
-GPU path's own generated code, checked before any GPU run."""
+skinny and direct kernels, transposed operands and fused epilogues, and the
+bf16 option's kernel -- the GPU path's own generated code, checked before any
+GPU run."""
 import numpy as np
 import pytest
 
@@ -68,3 +69,39 @@ def test_quad_kernel_on_host(tmp_path, M, K, N, ta, tb, epilogue, kernel):
     partial tiles added through LDS)."""
     src = _run(tmp_path, M, K, N, ta, tb, epilogue)
     assert kernel in src
+
+
+def _bf16(x):
+    """float32 -> bfloat16 (round to nearest even) -> float64."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32).astype(np.float64)
+
+
+@pytest.mark.parametrize("M,K,N,ta,tb", [(64, 64, 64, False, False), (130, 70, 257, True, True),
+                                         (96, 200, 100, False, True)])
+def test_bf16_kernel_on_host(tmp_path, M, K, N, ta, tb):
+    """The bf16 DotProd option (operands packed to k-contiguous bfloat16,
+    v_mfma_f32_32x32x16_bf16, fp32 sums) against float64 products of the
+    same bfloat16-rounded operands: only the fp32 summation differs, so
+    the bound is K eps (|A| @ |B|) -- far tighter than the rounding of the
+    operands themselves, which the check also sees."""
+    rng = np.random.default_rng(M * 13 + K * 5 + N)
+    a = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    b = rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    bias = rng.standard_normal((N,)).astype(np.float32)
+    ad.reset()
+    r = ((Tensor(a).T() if ta else Tensor(a)) @ (Tensor(b).T() if tb else Tensor(b))) + Tensor(bias)
+    Receiver(lambda v: None, [r])
+    dev, arena = host_arena(ad.compile_proc(), str(tmp_path), lockstep=True, dot_precision="bf16", bf16_min_macs=0)
+    assert arena is not None, "a launch left the arena or a barrier timed out"
+    assert any("dp_bf16<" in p.source for ps in dev.kernels.values() for p in ps)
+    off, nb = dev.ctx.reads[0]
+    got = arena[off:off + nb].view(np.float32).reshape(M, N)
+    a64, b64 = (_bf16(a).T if ta else _bf16(a)), (_bf16(b).T if tb else _bf16(b))
+    ref = a64 @ b64 + bias
+    bound = (K + 2) * np.finfo(np.float32).eps * (np.abs(a64) @ np.abs(b64) + np.abs(bias)) + 1e-7
+    err = np.abs(got - ref)
+    assert np.all(err <= bound), f"{np.max(err / bound):.2f} x the bound"
+    exact = (a.T if ta else a).astype(np.float64) @ (b.T if tb else b).astype(np.float64) + bias
+    assert np.max(np.abs(got - exact)) > 10 * np.max(bound), "the operands were not rounded to bfloat16"
