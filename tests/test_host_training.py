@@ -17,11 +17,11 @@ from oracle import OracleDevice
 from .host_emulation import host_values
 
 
-def _host_and_oracle(tmp_path, build):
+def _host_and_oracle(tmp_path, build, **device_options):
     ad.reset()
     start = build()
     init = [np.array(t.arr, dtype=np.float32).copy() for t in start["params_ref"]] if "params_ref" in start else None
-    vals = host_values(ad.compile_proc(), str(tmp_path), lockstep=True)
+    vals = host_values(ad.compile_proc(), str(tmp_path), lockstep=True, **device_options)
     assert vals is not None, "a launch left the arena or a barrier timed out"
     ad.reset()
     ref = build()
@@ -68,16 +68,22 @@ def test_layernorm_training_steps_on_host(tmp_path):
     assert np.max(np.abs(gamma - 1.0)) > 1e-2 and np.max(np.abs(beta)) > 1e-2
 
 
-@pytest.mark.parametrize("feeder", [True])
-def test_encoder_training_steps_on_host(tmp_path, feeder):
+@pytest.mark.parametrize("options", [
+    {},
+    {"arena": "unpacked", "graph_dag": True, "stream_min_bytes": 4096},
+    {"use_graphs": False, "group_launches": False, "narrow_launches": False},
+], ids=["default", "unpacked-dag-streaming", "eager-ungrouped"])
+def test_encoder_training_steps_on_host(tmp_path, options):
     """Two steps of a batched encoder layer (2 sequences of 8 rows, d_model
     32, 2 heads, ff 64) with its input fed each step: the per-head and
     attention products, softmax and LayerNorm reductions, the gradient sums
-    and the SGD updates.  The learning rate is large so that the updates
-    stand far above float32 rounding of the weights."""
+    and the SGD updates -- with the device's defaults, with the unpacked
+    arena, dependency-graph replay and nontemporal reads, and launch by
+    launch without graphs or grouping.  The learning rate is large so that
+    the updates stand far above float32 rounding of the weights."""
     build = lambda: workloads.transformer(layers=1, d_model=32, heads=2, ff=64, seq=8, batch=2,
-                                          steps=2, lr=10.0, feeder=feeder)
-    got, want, init = _host_and_oracle(tmp_path, build)
+                                          steps=2, lr=10.0, feeder=True)
+    got, want, init = _host_and_oracle(tmp_path, build, **options)
     assert len(got) == len(want) == 15
     for g, w, w0 in zip(got, want, init):
         moved = np.max(np.abs(w - w0.reshape(w.shape)))
