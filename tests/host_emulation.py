@@ -70,15 +70,15 @@ template <class F> static void adhip_launch(F f, const unsigned long long* t, un
 """
 
 
-# The same kernels with real values: every thread of a block runs on its own
-# OS thread; __syncthreads is a block barrier; a wavefront-scope fence is a
-# wave barrier; a shuffle or an fp32 MFMA exchanges the wave's values between
-# two wave barriers.  v_mfma_f32_32x32x2f32
-# takes A[i][k] from lane i + 32k and B[k][j] from lane j + 32k and returns,
-# in lane l's element r, row 8*(r/4) + 4*(l/32) + r%4 of column l%32 of
-# C + A*B; v_mfma_f32_32x32x16_bf16 takes eight k per lane (k = 8*(l/32) + v)
-# and returns the same layout.  A barrier waited on for 20 s aborts (a divergent barrier would
-# otherwise hang).  Blocks run one after another.
+# The same kernels with real values: every thread of a block runs as a fiber
+# of its own; __syncthreads is a block barrier; a wavefront-scope fence is a
+# wave barrier; a shuffle or an MFMA exchanges the wave's values between two
+# wave barriers.  v_mfma_f32_32x32x2f32 takes A[i][k] from lane i + 32k and
+# B[k][j] from lane j + 32k and returns, in lane l's element r, row
+# 8*(r/4) + 4*(l/32) + r%4 of column l%32 of C + A*B;
+# v_mfma_f32_32x32x16_bf16 takes eight k per lane (k = 8*(l/32) + v) and
+# returns the same layout.  A barrier that no thread can pass (a divergent
+# barrier) aborts the run.  Blocks run one after another.
 LOCKSTEP_SHIM = r"""
 #include <cstdint>
 #include <cstddef>
@@ -86,12 +86,11 @@ LOCKSTEP_SHIM = r"""
 #include <cstdlib>
 #include <cmath>
 #include <cstring>
-#include <thread>
-#include <mutex>
-#include <condition_variable>
-#include <chrono>
 #include <vector>
-#include <functional>
+#include <ucontext.h>
+#include <sys/mman.h>
+#include <sanitizer/common_interface_defs.h>
+#include <sanitizer/asan_interface.h>
 #define __global__
 #define __device__
 #define __host__
@@ -99,23 +98,93 @@ LOCKSTEP_SHIM = r"""
 #define __launch_bounds__(...)
 #define __shared__ static
 struct adhip_dim3 { unsigned x, y, z; };
-static thread_local adhip_dim3 threadIdx, blockIdx;
-static adhip_dim3 blockDim, gridDim;
+static adhip_dim3 threadIdx, blockIdx, blockDim, gridDim;
 struct float4 { float x, y, z, w; };
 static inline float4 make_float4(float a, float b, float c, float d) { float4 r; r.x = a; r.y = b; r.z = c; r.w = d; return r; }
 struct uint4 { unsigned x, y, z, w; };
 typedef float adhip_v16 __attribute__((ext_vector_type(16)));
+// Every thread of a block is a fiber (ucontext) of the one OS thread: a
+// fiber runs until it waits at a barrier or ends, then the next fiber of the
+// block that may go on resumes (the stack switches are announced to
+// AddressSanitizer).  A barrier no fiber can pass aborts the run.
+struct adhip_barrier;
+struct adhip_fiber {
+  ucontext_t ctx;
+  char* stack;
+  void* fake;
+  unsigned tid;
+  bool done;
+  adhip_barrier* bar;
+  unsigned gen;
+};
+static const size_t ADHIP_STACK = 256 * 1024;
+static ucontext_t adhip_sched;
+static const void* adhip_main_bottom = nullptr;
+static size_t adhip_main_size = 0;
+static std::vector<adhip_fiber> adhip_fibers;
+static adhip_fiber* adhip_cur = nullptr;
+static void (*adhip_kernel)(const unsigned long long*) = nullptr;
+static const unsigned long long* adhip_table = nullptr;
+static void adhip_yield() {
+  adhip_fiber* f = adhip_cur;
+  __sanitizer_start_switch_fiber(&f->fake, adhip_main_bottom, adhip_main_size);
+  swapcontext(&f->ctx, &adhip_sched);
+  __sanitizer_finish_switch_fiber(f->fake, nullptr, nullptr);
+}
+static void adhip_fiber_main() {
+  __sanitizer_finish_switch_fiber(nullptr, &adhip_main_bottom, &adhip_main_size);
+  adhip_kernel(adhip_table);
+  adhip_cur->done = true;
+  __sanitizer_start_switch_fiber(nullptr, adhip_main_bottom, adhip_main_size);
+}   // returns to adhip_sched (uc_link)
 struct adhip_barrier {
-  std::mutex m; std::condition_variable cv; unsigned n = 0, count = 0, gen = 0;
+  unsigned n = 0, count = 0, gen = 0;
   void wait() {
-    std::unique_lock<std::mutex> lk(m);
-    unsigned g = gen;
-    if (++count == n) { count = 0; ++gen; cv.notify_all(); return; }
-    if (!cv.wait_for(lk, std::chrono::seconds(20), [&] { return gen != g; })) {
-      fprintf(stderr, "barrier timeout\n"); abort();
-    }
+    if (++count == n) { count = 0; ++gen; return; }
+    adhip_cur->bar = this;
+    adhip_cur->gen = gen;
+    adhip_yield();
   }
 };
+static void adhip_run_block(unsigned bx) {
+  while (adhip_fibers.size() < bx) {
+    adhip_fiber f{};
+    void* st = mmap(nullptr, ADHIP_STACK, PROT_READ | PROT_WRITE, MAP_PRIVATE | MAP_ANONYMOUS, -1, 0);
+    if (st == MAP_FAILED) { fprintf(stderr, "fiber stack\n"); abort(); }
+    f.stack = (char*)st;
+    f.tid = adhip_fibers.size();
+    adhip_fibers.push_back(f);
+  }
+  for (unsigned i = 0; i < bx; ++i) {
+    adhip_fiber& f = adhip_fibers[i];
+    f.done = false; f.bar = nullptr; f.fake = nullptr;
+    __asan_unpoison_memory_region(f.stack, ADHIP_STACK);
+    getcontext(&f.ctx);
+    f.ctx.uc_stack.ss_sp = f.stack;
+    f.ctx.uc_stack.ss_size = ADHIP_STACK;
+    f.ctx.uc_link = &adhip_sched;
+    makecontext(&f.ctx, adhip_fiber_main, 0);
+  }
+  unsigned left = bx, i = 0, stuck = 0;
+  while (left) {
+    adhip_fiber& f = adhip_fibers[i];
+    if (!f.done && (!f.bar || f.bar->gen != f.gen)) {
+      f.bar = nullptr;
+      adhip_cur = &f;
+      threadIdx = {f.tid, 0, 0};
+      void* fake = nullptr;
+      __sanitizer_start_switch_fiber(&fake, f.stack, ADHIP_STACK);
+      swapcontext(&adhip_sched, &f.ctx);
+      __sanitizer_finish_switch_fiber(fake, nullptr, nullptr);
+      if (f.done) --left;
+      stuck = 0;
+    } else if (++stuck > bx) {
+      fprintf(stderr, "barrier deadlock\n");
+      abort();
+    }
+    i = i + 1 == bx ? 0 : i + 1;
+  }
+}
 static adhip_barrier adhip_block_bar;
 static adhip_barrier adhip_wave_bar[16];
 static float adhip_wave_a[16][64], adhip_wave_b[16][64];
@@ -175,48 +244,17 @@ template <class V> static inline adhip_v16 adhip_mfma_32x32x16_bf16(V a, V b, ad
 #define __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, ...) adhip_mfma_32x32x2((a), (b), (c))
 #define __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, ...) adhip_mfma_32x32x16_bf16((a), (b), (c))
 using std::exp2; using std::log2; using std::sin; using std::sqrt; using std::fabs;
-// one OS thread per thread of a block, kept across blocks and launches:
-// run(n, job) hands job(i) to threads 0..n-1 and returns when all are done
-struct adhip_pool {
-  std::mutex m; std::condition_variable go, fin;
-  std::vector<std::thread> lanes;
-  unsigned gen = 0, active = 0, left = 0;
-  std::function<void(unsigned)> job;
-  void work(unsigned i) {
-    unsigned seen = 0;
-    for (;;) {
-      std::function<void(unsigned)> j;
-      {
-        std::unique_lock<std::mutex> lk(m);
-        go.wait(lk, [&] { return gen != seen; });
-        seen = gen;
-        if (i >= active) continue;
-        j = job;
-      }
-      j(i);
-      std::lock_guard<std::mutex> lk(m);
-      if (--left == 0) fin.notify_one();
-    }
-  }
-  void run(unsigned n, std::function<void(unsigned)> f) {
-    while (lanes.size() < n) {
-      const unsigned i = lanes.size();
-      lanes.emplace_back([this, i] { work(i); });
-    }
-    std::unique_lock<std::mutex> lk(m);
-    job = std::move(f); active = n; left = n; ++gen;
-    go.notify_all();
-    fin.wait(lk, [&] { return left == 0; });
-  }
-};
-static adhip_pool* adhip_lanes = new adhip_pool;   // never destroyed: its threads wait at exit
 template <class F> static void adhip_launch(F f, const unsigned long long* t, unsigned gx, unsigned gy,
                                             unsigned gz, unsigned bx) {
   gridDim = {gx, gy, gz}; blockDim = {bx, 1, 1};
   adhip_block_bar.n = bx;
   for (unsigned w = 0; w < 16; ++w) adhip_wave_bar[w].n = (bx - 64 * w) < 64 ? (bx > 64 * w ? bx - 64 * w : 0) : 64;
-  for (unsigned z = 0; z < gz; ++z) for (unsigned y = 0; y < gy; ++y) for (unsigned x = 0; x < gx; ++x)
-    adhip_lanes->run(bx, [=](unsigned i) { blockIdx = {x, y, z}; threadIdx = {i, 0, 0}; f(t); });
+  adhip_kernel = f;
+  adhip_table = t;
+  for (unsigned z = 0; z < gz; ++z) for (unsigned y = 0; y < gy; ++y) for (unsigned x = 0; x < gx; ++x) {
+    blockIdx = {x, y, z};
+    adhip_run_block(bx);
+  }
 }
 """
 

@@ -1,5 +1,5 @@
 """DotProd kernels computed on the host in lockstep (every thread of a block
-on its own OS thread, real barriers, the fp32 MFMA and cross-lane shuffles
+a fiber of its own, real barriers, the MFMAs and cross-lane shuffles
 emulated with the hardware's lane layout; ``host_emulation.LOCKSTEP_SHIM``)
 against float64 numpy: the MFMA tile kernels (64 x 64 and 128 x 128 tiles,
 split K with its combine pass), ``dp_quad`` for small launch groups, the
