@@ -105,8 +105,10 @@ struct uint4 { unsigned x, y, z, w; };
 typedef float adhip_v16 __attribute__((ext_vector_type(16)));
 // Every thread of a block is a fiber (ucontext) of the one OS thread: a
 // fiber runs until it waits at a barrier or ends, then the next fiber of the
-// block that may go on resumes (the stack switches are announced to
-// AddressSanitizer).  A barrier no fiber can pass aborts the run.
+// block that may go on resumes, in ascending thread order (descending with
+// ADHIP_DESCENDING: data shared between threads without a barrier between
+// the write and the read then gives other results).  The stack switches are
+// announced to AddressSanitizer.  A barrier no fiber can pass aborts the run.
 struct adhip_barrier;
 struct adhip_fiber {
   ucontext_t ctx;
@@ -165,7 +167,11 @@ static void adhip_run_block(unsigned bx) {
     f.ctx.uc_link = &adhip_sched;
     makecontext(&f.ctx, adhip_fiber_main, 0);
   }
+#ifdef ADHIP_DESCENDING
+  unsigned left = bx, i = bx - 1, stuck = 0;
+#else
   unsigned left = bx, i = 0, stuck = 0;
+#endif
   while (left) {
     adhip_fiber& f = adhip_fibers[i];
     if (!f.done && (!f.bar || f.bar->gen != f.gen)) {
@@ -182,7 +188,11 @@ static void adhip_run_block(unsigned bx) {
       fprintf(stderr, "barrier deadlock\n");
       abort();
     }
+#ifdef ADHIP_DESCENDING
+    i = i == 0 ? bx - 1 : i - 1;
+#else
     i = i + 1 == bx ? 0 : i + 1;
+#endif
   }
 }
 static adhip_barrier adhip_block_bar;
@@ -470,7 +480,7 @@ def _host_source(src):
 
 
 def check_run(proc, workdir, shrink=None, device=None, dump=None, lockstep=False, full=False,
-              **device_options):
+              descending=False, **device_options):
     """Run ``proc`` through a recording HIPDevice (loops replayed as
     recorded graphs), then check transfers and argument tables
     (``check_tables``) and run every launch on the host under
@@ -484,7 +494,9 @@ def check_run(proc, workdir, shrink=None, device=None, dump=None, lockstep=False
     With ``full`` the run is the device's own, in call order: every replay's
     launches and copies, host writes and staged Feeder data applied when
     they were made, and every host read and Receiver fetch saved when it was
-    made (to ``reads.bin`` in ``workdir``, in order).  Returns ``(ok, log)``."""
+    made (to ``reads.bin`` in ``workdir``, in order).  ``descending`` (with
+    ``lockstep``) resumes a block's threads in descending order.  Returns
+    ``(ok, log)``."""
     dev = device or recording_device(**device_options)
     mark = len(dev.ctx.launches)
     dev.ctx.writes = []
@@ -508,7 +520,8 @@ def check_run(proc, workdir, shrink=None, device=None, dump=None, lockstep=False
         blob[off:off + len(data)] = data
     size = ctx.size - (shrink or 0)
     used = {op[1] for op in launches if op[0] == "launch"}
-    text = [LOCKSTEP_SHIM if lockstep else SHIM, _host_source(open(HEADER_PATH).read())]
+    text = [("#define ADHIP_DESCENDING 1\n" if descending else "") + (LOCKSTEP_SHIM if lockstep else SHIM),
+            _host_source(open(HEADER_PATH).read())]
     for i, (name, src) in enumerate(sources.items()):
         if name in used:
             text.append(f"namespace k{i} {{\n{_host_source(src)}\n}}\nusing k{i}::{name};")
@@ -576,19 +589,20 @@ def check_run(proc, workdir, shrink=None, device=None, dump=None, lockstep=False
     return r.returncode == 0 and "all launches in bounds" in r.stderr, r.stderr[-4000:]
 
 
-def host_arena(proc, workdir, lockstep=False, full=False, **device_options):
+def host_arena(proc, workdir, lockstep=False, full=False, descending=False, **device_options):
     """Run ``proc``'s launches on the host (``check_run``) and return the
     recording device and the arena bytes after the last launch (None if a
     launch leaves the arena)."""
     dump = os.path.join(workdir, "arena_after.bin")
     dev = recording_device(**device_options)
-    ok, log = check_run(proc, workdir, device=dev, dump=dump, lockstep=lockstep, full=full)
+    ok, log = check_run(proc, workdir, device=dev, dump=dump, lockstep=lockstep, full=full,
+                        descending=descending)
     if not ok:
         print(log[-2000:])
     return dev, (np.fromfile(dump, dtype=np.uint8) if ok else None)
 
 
-def host_values(proc, workdir, lockstep=False, **device_options):
+def host_values(proc, workdir, lockstep=False, descending=False, **device_options):
     """Values of every host read of a Proc (top-level Receivers, Receivers
     inside loops once per iteration, the final Tensor read-back) computed
     by running the device's whole run on the host (``check_run`` with
@@ -597,7 +611,8 @@ def host_values(proc, workdir, lockstep=False, **device_options):
     exchange data (elementwise passes, operand gathers, copies) compute
     real values: cross-lane and MFMA builtins return their inputs and a
     block's threads run one after another."""
-    dev, arena = host_arena(proc, workdir, lockstep=lockstep, full=True, **device_options)
+    dev, arena = host_arena(proc, workdir, lockstep=lockstep, full=True, descending=descending,
+                            **device_options)
     if arena is None:
         return None
     blob = np.fromfile(os.path.join(workdir, "reads.bin"), dtype=np.uint8)

@@ -1,0 +1,55 @@
+"""Data shared between the threads of a block is ordered by barriers: the
+generated kernels run on the host in lockstep twice, with the block's
+threads resumed in ascending and in descending order between barriers
+(``host_emulation`` with ``descending``), and every host read is
+bit-identical.  A write to LDS read by another thread without a barrier in
+between gives different results in the two orders, and the same holds for
+lanes of one wave that exchange data without a wavefront fence."""
+import numpy as np
+import pytest
+
+import ad_amd as ad
+from ad_amd import workloads
+from ad_amd.graph import Receiver, Tensor
+
+from .host_emulation import host_values
+
+
+def _product(M, K, N, ta, tb):
+    """A product with a fused epilogue and both reductions of it."""
+    rng = np.random.default_rng(M + K + N)
+    a = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    b = rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    A, B = Tensor(a), Tensor(b)
+    r = (A.T() if ta else A) @ (B.T() if tb else B)
+    Receiver(lambda *v: None, [(r + 1.0).sigmoid(), r.sum(0), r.sum(1)])
+
+
+CASES = {
+    "layernorm-training": (lambda: workloads.layernorm_train(rows=64, cols=256, steps=2), {}, "reduce_rows<"),
+    "tile64": (lambda: _product(130, 300, 257, True, False), {"narrow_launches": False}, "dp_mfma<64, 64"),
+    "tile128": (lambda: _product(520, 136, 520, True, True), {"narrow_launches": False}, "dp_mfma<128, 128"),
+    "quad": (lambda: _product(130, 300, 257, True, True), {}, "dp_quad<1, 128>"),
+    "quad-split": (lambda: _product(64, 1024, 64, False, True), {}, "dp_quad<4, 128>"),
+    "bf16": (lambda: _product(130, 70, 257, True, True), {"dot_precision": "bf16", "bf16_min_macs": 0}, "dp_bf16<"),
+}
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_thread_order_does_not_change_results(tmp_path, name):
+    build, options, kernel = CASES[name]
+    runs = []
+    for descending in (False, True):
+        ad.reset()
+        build()
+        proc = ad.compile_proc()
+        workdir = tmp_path / ("descending" if descending else "ascending")
+        workdir.mkdir()
+        runs.append(host_values(proc, str(workdir), lockstep=True, descending=descending, **options))
+        assert runs[-1] is not None, "a launch left the arena or a barrier no thread could pass"
+    sources = " ".join(open(p).read() for p in tmp_path.glob("ascending/run_*.cpp"))
+    assert kernel in sources
+    up, down = runs
+    assert len(up) == len(down) > 0
+    for x, y in zip(up, down):
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
