@@ -262,7 +262,11 @@ template <class F> static void adhip_launch(F f, const unsigned long long* t, un
   adhip_kernel = f;
   adhip_table = t;
   for (unsigned z = 0; z < gz; ++z) for (unsigned y = 0; y < gy; ++y) for (unsigned x = 0; x < gx; ++x) {
+#ifdef ADHIP_DESCENDING
+    blockIdx = {gx - 1 - x, gy - 1 - y, gz - 1 - z};
+#else
     blockIdx = {x, y, z};
+#endif
     adhip_run_block(bx);
   }
 }
@@ -495,8 +499,8 @@ def check_run(proc, workdir, shrink=None, device=None, dump=None, lockstep=False
     launches and copies, host writes and staged Feeder data applied when
     they were made, and every host read and Receiver fetch saved when it was
     made (to ``reads.bin`` in ``workdir``, in order).  ``descending`` (with
-    ``lockstep``) resumes a block's threads in descending order.  Returns
-    ``(ok, log)``."""
+    ``lockstep``) runs a launch's blocks, and resumes a block's threads, in
+    descending order.  Returns ``(ok, log)``."""
     dev = device or recording_device(**device_options)
     mark = len(dev.ctx.launches)
     dev.ctx.writes = []

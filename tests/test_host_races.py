@@ -1,10 +1,12 @@
-"""Data shared between the threads of a block is ordered by barriers: the
-generated kernels run on the host in lockstep twice, with the block's
-threads resumed in ascending and in descending order between barriers
-(``host_emulation`` with ``descending``), and every host read is
-bit-identical.  A write to LDS read by another thread without a barrier in
-between gives different results in the two orders, and the same holds for
-lanes of one wave that exchange data without a wavefront fence."""
+"""Data shared between the threads of a block is ordered by barriers, and
+the blocks of a launch do not depend on each other: the generated kernels
+run on the host in lockstep twice, with a launch's blocks run and a block's
+threads resumed in ascending and in descending order (``host_emulation``
+with ``descending``), and every host read is bit-identical.  A write to LDS
+read by another thread without a barrier in between gives different results
+in the two orders, as do lanes of one wave that exchange data without a
+wavefront fence, and blocks (or grouped instances of one launch) that read
+what another block of the launch writes."""
 import numpy as np
 import pytest
 
@@ -27,6 +29,8 @@ def _product(M, K, N, ta, tb):
 
 CASES = {
     "layernorm-training": (lambda: workloads.layernorm_train(rows=64, cols=256, steps=2), {}, "reduce_rows<"),
+    "encoder-training": (lambda: workloads.transformer(layers=1, d_model=32, heads=2, ff=64, seq=8, batch=2,
+                                                       steps=2, lr=10.0, feeder=True), {}, "reduce_cols<"),
     "tile64": (lambda: _product(130, 300, 257, True, False), {"narrow_launches": False}, "dp_mfma<64, 64"),
     "tile128": (lambda: _product(520, 136, 520, True, True), {"narrow_launches": False}, "dp_mfma<128, 128"),
     "quad": (lambda: _product(130, 300, 257, True, True), {}, "dp_quad<1, 128>"),
