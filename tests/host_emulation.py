@@ -325,7 +325,15 @@ class RecordingContext:
 
     def launcher(self, func, grid, block, shared, args):
         return lambda *_: self._sink().append(("launch", func, tuple(grid), tuple(block), shared, args[0]))
-    launcher_on = launcher
+
+    def launcher_on(self, func, grid, block, shared, args):
+        """As ``launcher``; a launch on another stream than 0 is preceded by
+        a ``("lane", stream)`` mark."""
+        def go(stream=0):
+            if stream:
+                self._sink().append(("lane", stream))
+            self._sink().append(("launch", func, tuple(grid), tuple(block), shared, args[0]))
+        return go
 
     def graph_begin(self):
         if self._capture is not None:
@@ -415,14 +423,64 @@ class RecordingContext:
 
     def lanes_reserve(self, *a): pass
     def sync(self): pass
-    def record_on(self, *a): pass
-    def wait_on(self, *a): pass
+    def record_on(self, stream, event):
+        self._sink().append(("record", stream, event))
+
+    def wait_on(self, stream, event):
+        self._sink().append(("wait", stream, event))
 
     def close(self):
         self.h = None
 
 
 _NARGS_RE = re.compile(r"blockIdx\.z \* (\d+)u")
+
+
+def lanes_late_first(ops):
+    """The recorded operations in another order the streams allow: at each
+    step the highest-numbered stream whose next operation may start runs
+    it (a wait may start once the latest earlier record of its event has
+    run).  Host transfers (writes, reads) keep their place: everything
+    issued before one runs before it.  Launches, copies, records and waits
+    of stream 0 keep their order, as do those of each other stream."""
+    out, segment = [], []
+
+    def drain():
+        seq, queues, last_record = [], {}, {}
+        lane = 0
+        for op in segment:
+            if op[0] == "lane":
+                lane = op[1]
+                continue
+            on = op[1] if op[0] in ("record", "wait") else (lane if op[0] == "launch" else 0)
+            lane = 0 if op[0] == "launch" else lane
+            dep = last_record.get(op[2]) if op[0] == "wait" else None
+            if op[0] == "record":
+                last_record[op[2]] = len(seq)
+            queues.setdefault(on, []).append(len(seq))
+            seq.append((op, dep))
+        done, heads = set(), {q: 0 for q in queues}
+        while len(done) < len(seq):
+            for q in sorted(queues, reverse=True):
+                if heads[q] < len(queues[q]):
+                    i = queues[q][heads[q]]
+                    if seq[i][1] is None or seq[i][1] in done:
+                        break
+            else:
+                raise AssertionError("the streams' waits admit no order")
+            heads[q] += 1
+            done.add(i)
+            out.append(seq[i][0])
+        segment.clear()
+
+    for op in ops:
+        if op[0] in ("write", "read"):
+            drain()
+            out.append(op)
+        else:
+            segment.append(op)
+    drain()
+    return out
 
 
 def check_tables(dev, ctx, sources):
@@ -498,9 +556,10 @@ def check_run(proc, workdir, shrink=None, device=None, dump=None, lockstep=False
     With ``full`` the run is the device's own, in call order: every replay's
     launches and copies, host writes and staged Feeder data applied when
     they were made, and every host read and Receiver fetch saved when it was
-    made (to ``reads.bin`` in ``workdir``, in order).  ``descending`` (with
-    ``lockstep``) runs a launch's blocks, and resumes a block's threads, in
-    descending order.  Returns ``(ok, log)``."""
+    made (to ``reads.bin`` in ``workdir``, in order).  ``descending`` runs
+    the operations of several streams late stream first
+    (``lanes_late_first``) and, with ``lockstep``, a launch's blocks and a
+    block's threads in descending order.  Returns ``(ok, log)``."""
     dev = device or recording_device(**device_options)
     mark = len(dev.ctx.launches)
     dev.ctx.writes = []
@@ -518,6 +577,8 @@ def check_run(proc, workdir, shrink=None, device=None, dump=None, lockstep=False
         ctx.launches = saved
     if bad:
         return False, f"argument tables: {bad[:5]}"
+    if descending:
+        launches = lanes_late_first(launches)
     os.makedirs(workdir, exist_ok=True)
     blob = bytearray(ctx.size)
     for off, data in ctx.writes:
@@ -567,6 +628,8 @@ def check_run(proc, workdir, shrink=None, device=None, dump=None, lockstep=False
         if op[0] == "read":
             if full:
                 text.append(f"  if (fwrite(a + {op[1]}ull, 1, {op[2]}ull, rd) != {op[2]}ull) return 7;")
+            continue
+        if op[0] in ("lane", "record", "wait"):
             continue
         _, func, grid, block, shared, row = op
         if not full and (func, grid, row) in seen:
