@@ -289,6 +289,8 @@ class RecordingContext:
         self.writes, self.launches, self.errors = [], [], []
         self.reads = []                # (arena offset, bytes) of every host read, in order
         self._capture = None           # launches of the graph being captured
+        self.dag_late = False          # replay dependency graphs latest-node first
+        self._late = {}                # graph -> its nodes in that order
         self._graphs = {}
         self._staging = {}             # tag -> open
         self._fetch = {}               # set -> (capacity, used, open, pending)
@@ -358,10 +360,14 @@ class RecordingContext:
             if any(not 0 <= j < i for j in d):
                 self.errors.append(("dependency on a later node", i, list(d), 0))
         self.dags = getattr(self, "dags", []) + [[list(d) for d in deps]]
-        return self.graph_end()
+        nodes = [op for op in self._capture if not any(op is c for c in captured)] + \
+            _latest_ready_first(captured, deps)
+        g = self.graph_end()
+        self._late[g] = nodes
+        return g
 
     def graph_launch(self, g):
-        self.launches.extend(self._graphs[g])
+        self.launches.extend(self._late[g] if self.dag_late and g in self._late else self._graphs[g])
 
     def graph_destroy(self, g):
         self._graphs.pop(g, None)
@@ -434,6 +440,17 @@ class RecordingContext:
 
 
 _NARGS_RE = re.compile(r"blockIdx\.z \* (\d+)u")
+
+
+def _latest_ready_first(nodes, deps):
+    """The nodes of a dependency graph in the order that always runs the
+    highest-numbered node whose dependencies have all run."""
+    done, order = set(), []
+    while len(order) < len(nodes):
+        i = max(j for j in range(len(nodes)) if j not in done and all(d in done for d in deps[j]))
+        done.add(i)
+        order.append(nodes[i])
+    return order
 
 
 def lanes_late_first(ops):
@@ -558,9 +575,11 @@ def check_run(proc, workdir, shrink=None, device=None, dump=None, lockstep=False
     they were made, and every host read and Receiver fetch saved when it was
     made (to ``reads.bin`` in ``workdir``, in order).  ``descending`` runs
     the operations of several streams late stream first
-    (``lanes_late_first``) and, with ``lockstep``, a launch's blocks and a
+    (``lanes_late_first``), the nodes of dependency-graph replays latest
+    ready node first, and, with ``lockstep``, a launch's blocks and a
     block's threads in descending order.  Returns ``(ok, log)``."""
     dev = device or recording_device(**device_options)
+    dev.ctx.dag_late = descending
     mark = len(dev.ctx.launches)
     dev.ctx.writes = []
     dev.ctx.reads = []

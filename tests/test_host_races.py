@@ -33,6 +33,8 @@ CASES = {
     "layernorm-training": (lambda: workloads.layernorm_train(rows=64, cols=256, steps=2), {}, "reduce_rows<"),
     "encoder-training": (lambda: workloads.transformer(layers=1, d_model=32, heads=2, ff=64, seq=8, batch=2,
                                                        steps=2, lr=10.0, feeder=True), {}, "reduce_cols<"),
+    "encoder-training-dag": (lambda: workloads.transformer(layers=2, d_model=32, heads=2, ff=64, seq=8, batch=2,
+                                                           steps=2, lr=10.0), {"graph_dag": True}, "reduce_cols<"),
     "tile64": (lambda: _product(130, 300, 257, True, False), {"narrow_launches": False}, "dp_mfma<64, 64"),
     "tile128": (lambda: _product(520, 136, 520, True, True), {"narrow_launches": False}, "dp_mfma<128, 128"),
     "quad": (lambda: _product(130, 300, 257, True, True), {}, "dp_quad<1, 128>"),
