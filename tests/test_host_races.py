@@ -8,7 +8,8 @@ in the two orders, as do lanes of one wave that exchange data without a
 wavefront fence, and blocks (or grouped instances of one launch) that read
 what another block of the launch writes.  Runs on several streams are also
 replayed with the later streams' work moved as early as their event waits
-allow."""
+allow, and loop bodies replayed as dependency graphs with the latest ready
+node run first."""
 import numpy as np
 import pytest
 
