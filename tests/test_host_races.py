@@ -32,10 +32,10 @@ def _product(M, K, N, ta, tb):
 
 CASES = {
     "layernorm-training": (lambda: workloads.layernorm_train(rows=64, cols=256, steps=2), {}, "reduce_rows<"),
-    "encoder-training": (lambda: workloads.transformer(layers=1, d_model=32, heads=2, ff=64, seq=8, batch=2,
-                                                       steps=2, lr=10.0, feeder=True), {}, "reduce_cols<"),
-    "encoder-training-dag": (lambda: workloads.transformer(layers=2, d_model=32, heads=2, ff=64, seq=8, batch=2,
-                                                           steps=2, lr=10.0), {"graph_dag": True}, "reduce_cols<"),
+    # grouped launches, and the loop body replayed as a dependency graph
+    "encoder-training-dag": (lambda: workloads.transformer(layers=1, d_model=32, heads=2, ff=64, seq=8, batch=2,
+                                                           steps=2, lr=10.0, feeder=True), {"graph_dag": True},
+                             "reduce_cols<"),
     "tile64": (lambda: _product(130, 300, 257, True, False), {"narrow_launches": False}, "dp_mfma<64, 64"),
     "tile128": (lambda: _product(520, 136, 520, True, True), {"narrow_launches": False}, "dp_mfma<128, 128"),
     "quad": (lambda: _product(130, 300, 257, True, True), {}, "dp_quad<1, 128>"),
@@ -66,14 +66,14 @@ def test_thread_order_does_not_change_results(tmp_path, name):
 
 def test_stream_waits_order_the_lanes(tmp_path):
     """Uncaptured runs on several streams (``lanes=4``, no graphs): two
-    training steps of a two-layer encoder run in the order the device
+    training steps of an encoder layer run in the order the device
     issues them and again with the operations of the later streams run as
     early as their event waits allow (``lanes_late_first``), blocks and
     threads in descending order.  Both agree bit for bit, and with the
     oracle: the waits the scheduler places order every dependent launch."""
     from oracle import OracleDevice
     from .host_emulation import recording_device
-    build = lambda: workloads.transformer(layers=2, d_model=32, heads=2, ff=64, seq=8, batch=2, steps=2,
+    build = lambda: workloads.transformer(layers=1, d_model=32, heads=2, ff=64, seq=8, batch=2, steps=2,
                                           lr=10.0, feeder=True)
     options = {"lanes": 4, "use_graphs": False}
     ad.reset()
